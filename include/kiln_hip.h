@@ -1,0 +1,148 @@
+/*
+ * kiln_hip.h — C ABI of the MI355X (gfx950) affine-quantized linear path.
+ *
+ * Drop-in for the four mlx-c entry points Kiln's quantized layers reach:
+ *
+ *   kh_quantized_matmul     replaces mlx_quantized_matmul, bound at
+ *                           crates/kiln-mlx/src/ops.rs:374-385 and wrapped by
+ *                           ops::quantized_matmul (ops.rs:359-388); callers
+ *                           Linear::forward (crates/kiln-models/src/nn.rs:89)
+ *                           and Embedding::as_linear (nn.rs:187).
+ *   kh_dequantize           replaces mlx_dequantize, bound at ops.rs:467-480
+ *                           (ops::dequantize, ops.rs:456-484).
+ *   kh_take                 replaces mlx_take_axis for axis 0, bound at
+ *                           ops.rs:250-254 (ops::take).
+ *   kh_quantized_embedding  the fused form of Embedding::lookup
+ *                           (nn.rs:159-176): three take(axis=0) calls
+ *                           followed by dequantize, in one pass.
+ *
+ * Conventions (mirroring crates/kiln-mlx/src/error.rs:24-72, array.rs):
+ *   - every call returns 0 on success and a non-zero kh_status on error; the
+ *     message of the last failing call on the calling thread is returned by
+ *     kh_last_error() (thread-local, valid until the next failing call on
+ *     that thread). No call aborts the process on bad input.
+ *   - arrays are plain descriptors of caller-owned, row-contiguous device
+ *     memory. Inputs are borrowed; the result `res` is caller-allocated with
+ *     the shape the operation produces (the call checks it) and its dtype
+ *     selects the output element type.
+ *   - all work is enqueued on the given HIP stream (NULL = the device's null
+ *     stream) and is asynchronous; the caller synchronises at its step
+ *     boundary, as Kiln does at eval/async_eval (array.rs:460-475).
+ *   - a stream is driven from one thread at a time; calls on different
+ *     streams may run concurrently.
+ *   - shapes follow MLX: x is [..., K] (leading dims flattened to M), w is
+ *     [N, K*bits/32] uint32 with the lowest `bits` bits holding the lowest
+ *     column, scales and biases are [N, K/group_size]. mode must be "affine"
+ *     (or NULL, meaning "affine").
+ */
+#ifndef KILN_HIP_H
+#define KILN_HIP_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types; the numbering follows mlx_dtype (mlx-c v0.6.0), of which
+ * Kiln uses the subset in crates/kiln-mlx/src/array.rs:22-69. */
+typedef enum kh_dtype {
+  KH_BOOL = 0,
+  KH_UINT8 = 1,
+  KH_UINT16 = 2,
+  KH_UINT32 = 3,
+  KH_UINT64 = 4,
+  KH_INT8 = 5,
+  KH_INT16 = 6,
+  KH_INT32 = 7,
+  KH_INT64 = 8,
+  KH_FLOAT16 = 9,
+  KH_FLOAT32 = 10,
+  KH_FLOAT64 = 11,
+  KH_BFLOAT16 = 12,
+  KH_COMPLEX64 = 13
+} kh_dtype;
+
+#define KH_MAX_NDIM 8
+
+/* A borrowed view of row-contiguous device memory. */
+typedef struct kh_array {
+  void* data;                 /* device pointer (HBM); may be NULL iff size 0 */
+  int32_t dtype;              /* kh_dtype */
+  int32_t ndim;               /* 0 .. KH_MAX_NDIM */
+  int64_t shape[KH_MAX_NDIM]; /* row-major, contiguous */
+} kh_array;
+
+/* mlx_optional_int: has_value=false selects the MLX default
+ * (group_size 64, bits 4). */
+typedef struct kh_optional_int {
+  int32_t value;
+  bool has_value;
+} kh_optional_int;
+
+/* Opaque HIP stream handle (hipStream_t). */
+typedef void* kh_stream;
+
+typedef enum kh_status {
+  KH_OK = 0,
+  KH_ERR_INVALID_ARGUMENT = 1, /* shape, dtype, bits/group_size/mode domain */
+  KH_ERR_UNSUPPORTED = 2,      /* valid MLX input this library does not run */
+  KH_ERR_DEVICE = 3,           /* HIP runtime error (launch, memory) */
+  KH_ERR_NO_DEVICE = 4         /* no usable gfx950 device */
+} kh_status;
+
+/* res = x @ dequantize(w, scales, biases)^T   (transpose = true)
+ * res = x @ dequantize(w, scales, biases)     (transpose = false)
+ *
+ * transpose=true (every Kiln call site): x [..., K], w [N, K*bits/32],
+ * scales/biases [N, K/gs], res [..., N].
+ * transpose=false: x [..., K], w [K, N*bits/32], scales/biases [K, N/gs],
+ * res [..., N].
+ * x: bfloat16 | float16 | float32; scales/biases: bfloat16 | float16 | float32
+ * (same dtype for both); res: bfloat16 | float16 | float32. Products are
+ * accumulated in float32 and rounded once (round-to-nearest-even) to res.
+ * bits in {4, 8}; group_size in {32, 64, 128}; K % group_size == 0. */
+int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
+                        const kh_array* scales, const kh_array* biases,
+                        bool transpose, kh_optional_int group_size,
+                        kh_optional_int bits, const char* mode,
+                        kh_stream stream);
+
+/* res[r, k] = round(fma(f32(scales[r, k/gs]), f32(q[r, k]), f32(biases[r, k/gs])))
+ * w [..., R, K*bits/32] -> res [..., R, K]; res dtype bfloat16|float16|float32
+ * (MLX's default is the scales dtype, ops.rs:476-479 leaves it unset). */
+int kh_dequantize(kh_array* res, const kh_array* w, const kh_array* scales,
+                  const kh_array* biases, kh_optional_int group_size,
+                  kh_optional_int bits, const char* mode, kh_stream stream);
+
+/* res = take(a, indices, axis=0): rows of a (any dtype, [V, ...]) gathered
+ * at indices (uint32 | int32, any shape) -> res [indices.shape..., a.shape[1:]...].
+ * Negative int32 indices count from the end (MLX's take). An index outside
+ * [-V, V) yields a zero row (HBM is never read out of bounds). */
+int kh_take(kh_array* res, const kh_array* a, const kh_array* indices,
+            kh_stream stream);
+
+/* res = dequantize(take(w, ids), take(scales, ids), take(biases, ids)):
+ * the quantized embedding lookup. ids uint32|int32 of any shape; w [V, H*bits/32];
+ * scales/biases [V, H/gs]; res [ids.shape..., H], bfloat16|float16|float32.
+ * Bit-identical to kh_take of the three tensors followed by kh_dequantize;
+ * out-of-range ids give zero rows as in kh_take. */
+int kh_quantized_embedding(kh_array* res, const kh_array* ids,
+                           const kh_array* w, const kh_array* scales,
+                           const kh_array* biases, kh_optional_int group_size,
+                           kh_optional_int bits, const char* mode,
+                           kh_stream stream);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* kh_last_error(void);
+
+/* Library version string. */
+const char* kh_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KILN_HIP_H */

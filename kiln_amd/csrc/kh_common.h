@@ -1,0 +1,69 @@
+// kh_common.h — shared device helpers for the gfx950 quantized-linear kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kiln_hip.h"
+
+namespace kh {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+// Element types the kernels read and write (values of kh_dtype).
+enum : int { DT_F16 = KH_FLOAT16, DT_F32 = KH_FLOAT32, DT_BF16 = KH_BFLOAT16 };
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// float -> bfloat16 bits, round-to-nearest-even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// float -> binary16 bits, round-to-nearest-even (hardware conversion).
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Load element i of a float array of dtype dt as float32 (exact).
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
+  if (dt == DT_F32) return static_cast<const float*>(p)[i];
+  uint32_t h = static_cast<const uint16_t*>(p)[i];
+  return dt == DT_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+
+// Round v to dtype dt and store it as element i.
+__device__ __forceinline__ void store_from_f32(void* p, int dt, int64_t i, float v) {
+  if (dt == DT_F32) {
+    static_cast<float*>(p)[i] = v;
+  } else {
+    uint32_t h = dt == DT_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+    static_cast<uint16_t*>(p)[i] = (uint16_t)h;
+  }
+}
+
+// Round a pair to dt and pack the two 16-bit results (lo = a).
+__device__ __forceinline__ uint32_t pack2(float a, float b, int dt) {
+  uint32_t ha = dt == DT_BF16 ? f32_to_bf16_bits(a) : f32_to_f16_bits(a);
+  uint32_t hb = dt == DT_BF16 ? f32_to_bf16_bits(b) : f32_to_f16_bits(b);
+  return ha | (hb << 16);
+}
+
+// v_perm_b32: byte i of the result is byte sel_i of the 8-byte value {hi, lo}.
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+}  // namespace kh

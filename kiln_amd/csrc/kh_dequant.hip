@@ -1,0 +1,228 @@
+// kh_dequant.hip — dequantize, quantized embedding gather, take, and the
+// general quantized matmul for gfx950.
+//
+// dequantize (crates/kiln-mlx/src/ops.rs:456-484) and the embedding lookup
+// (Embedding::lookup, crates/kiln-models/src/nn.rs:159-176: take x3 then
+// dequantize) are HBM-bound byte work: one thread expands one packed word
+// (8 four-bit or 4 eight-bit codes) with one float32 fma per code, rounds once
+// to the output type and writes the values with one vector store.
+#include "kh_common.h"
+#include "kh_kernels.h"
+
+namespace kh {
+
+namespace {
+
+// Round CPW values to odt and store them at out + base (vector store when
+// VEC, which the host selects when the output is suitably aligned).
+template <int CPW, bool VEC>
+__device__ __forceinline__ void store_codes(void* out, int odt, int64_t base, const float* v) {
+  if constexpr (VEC) {
+    if (odt == DT_F32) {
+      f32x4* o = reinterpret_cast<f32x4*>(static_cast<float*>(out) + base);
+#pragma unroll
+      for (int c = 0; c < CPW; c += 4) o[c / 4] = f32x4{v[c], v[c + 1], v[c + 2], v[c + 3]};
+    } else {
+      uint32_t p[CPW / 2];
+#pragma unroll
+      for (int c = 0; c < CPW; c += 2) p[c / 2] = pack2(v[c], v[c + 1], odt);
+      uint16_t* o16 = static_cast<uint16_t*>(out) + base;
+      if constexpr (CPW == 8) {
+        *reinterpret_cast<u32x4*>(o16) = u32x4{p[0], p[1], p[2], p[3]};
+      } else {
+        *reinterpret_cast<u32x2*>(o16) = u32x2{p[0], p[1]};
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) store_from_f32(out, odt, base + c, v[c]);
+  }
+}
+
+template <int BITS>
+__device__ __forceinline__ void expand_word(uint32_t u, float sc, float bi, float* v) {
+  constexpr int CPW = 32 / BITS;
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) v[c] = fmaf(sc, (float)((u >> (BITS * c)) & ((1u << BITS) - 1u)), bi);
+}
+
+template <int BITS, bool VEC>
+__global__ void dequant_kernel(const uint32_t* __restrict__ w, const void* __restrict__ scales,
+                               const void* __restrict__ biases, int sdt, void* __restrict__ out,
+                               int odt, int64_t R, int64_t K, int gs) {
+  constexpr int CPW = 32 / BITS;
+  const int64_t WR = K / CPW;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= R * WR) return;
+  const int64_t r = i / WR, wi = i % WR;
+  const int64_t G = K / gs;
+  const int64_t si = r * G + (wi * CPW) / gs;
+  float v[CPW];
+  expand_word<BITS>(__builtin_nontemporal_load(w + i), load_as_f32(scales, sdt, si),
+                    load_as_f32(biases, sdt, si), v);
+  store_codes<CPW, VEC>(out, odt, r * K + wi * CPW, v);
+}
+
+__device__ __forceinline__ int64_t resolve_id(const void* ids, bool ids_signed, int64_t t,
+                                              int64_t V) {
+  int64_t id = ids_signed ? (int64_t) static_cast<const int32_t*>(ids)[t]
+                          : (int64_t) static_cast<const uint32_t*>(ids)[t];
+  if (id < 0) id += V;
+  return (id < 0 || id >= V) ? -1 : id;
+}
+
+template <int BITS, bool VEC>
+__global__ void embedding_kernel(const void* __restrict__ ids, int ids_signed, int64_t T,
+                                 const uint32_t* __restrict__ w, const void* __restrict__ scales,
+                                 const void* __restrict__ biases, int sdt, void* __restrict__ out,
+                                 int odt, int64_t V, int64_t H, int gs) {
+  constexpr int CPW = 32 / BITS;
+  const int64_t WR = H / CPW;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * WR) return;
+  const int64_t t = i / WR, wi = i % WR;
+  const int64_t id = resolve_id(ids, ids_signed != 0, t, V);
+  float v[CPW];
+  if (id < 0) {
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) v[c] = 0.f;
+  } else {
+    const int64_t G = H / gs;
+    const int64_t si = id * G + (wi * CPW) / gs;
+    expand_word<BITS>(w[id * WR + wi], load_as_f32(scales, sdt, si), load_as_f32(biases, sdt, si),
+                      v);
+  }
+  store_codes<CPW, VEC>(out, odt, t * H + wi * CPW, v);
+}
+
+// take on rows of `units` elements of type U.
+template <typename U>
+__global__ void take_kernel(const U* __restrict__ a, int64_t V, int64_t units,
+                            const void* __restrict__ ids, int ids_signed, int64_t T,
+                            U* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * units) return;
+  const int64_t t = i / units, e = i % units;
+  const int64_t id = resolve_id(ids, ids_signed != 0, t, V);
+  if (id < 0) {
+    U z;
+    __builtin_memset(&z, 0, sizeof(U));
+    out[i] = z;
+  } else {
+    out[i] = a[id * units + e];
+  }
+}
+
+// General quantized matmul: one thread per output, acc = fma(x, w, acc) over
+// k in increasing order with w = fma(s, q, b) — the same float32 operation
+// sequence as the CPU oracle's restatement.
+template <int BITS>
+__global__ void qmm_generic_kernel(const void* __restrict__ x, int xdt,
+                                   const uint32_t* __restrict__ w, const void* __restrict__ scales,
+                                   const void* __restrict__ biases, int sdt, void* __restrict__ out,
+                                   int odt, int M, int N, int K, int gs, int transpose) {
+  constexpr int CPW = 32 / BITS;
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  for (int m = blockIdx.y; m < M; m += gridDim.y) {
+  float acc = 0.f;
+  if (transpose) {
+    const int64_t WR = K / CPW, G = K / gs;
+    const uint32_t* row = w + (int64_t)n * WR;
+    for (int k = 0; k < K; ++k) {
+      const float sc = load_as_f32(scales, sdt, (int64_t)n * G + k / gs);
+      const float bi = load_as_f32(biases, sdt, (int64_t)n * G + k / gs);
+      const float wv = fmaf(sc, (float)((row[k / CPW] >> (BITS * (k % CPW))) & MASK), bi);
+      acc = fmaf(load_as_f32(x, xdt, (int64_t)m * K + k), wv, acc);
+    }
+  } else {
+    const int64_t WR = N / CPW, G = N / gs;
+    for (int k = 0; k < K; ++k) {
+      const float sc = load_as_f32(scales, sdt, (int64_t)k * G + n / gs);
+      const float bi = load_as_f32(biases, sdt, (int64_t)k * G + n / gs);
+      const uint32_t word = w[(int64_t)k * WR + n / CPW];
+      const float wv = fmaf(sc, (float)((word >> (BITS * (n % CPW))) & MASK), bi);
+      acc = fmaf(load_as_f32(x, xdt, (int64_t)m * K + k), wv, acc);
+    }
+  }
+  store_from_f32(out, odt, (int64_t)m * N + n, acc);
+  }
+}
+
+inline unsigned blocks_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
+
+}  // namespace
+
+hipError_t launch_dequantize(const void* w, const void* scales, const void* biases, int sdt,
+                             void* out, int odt, int64_t R, int64_t K, int gs, int bits,
+                             hipStream_t stream) {
+  const int64_t words = R * (K * bits / 32);
+  if (words == 0) return hipSuccess;
+  const bool vec = (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+  const dim3 grid(blocks_for(words, 256)), block(256);
+  const uint32_t* wp = static_cast<const uint32_t*>(w);
+  if (bits == 4) {
+    if (vec) hipLaunchKernelGGL((dequant_kernel<4, true>), grid, block, 0, stream, wp, scales, biases, sdt, out, odt, R, K, gs);
+    else hipLaunchKernelGGL((dequant_kernel<4, false>), grid, block, 0, stream, wp, scales, biases, sdt, out, odt, R, K, gs);
+  } else {
+    if (vec) hipLaunchKernelGGL((dequant_kernel<8, true>), grid, block, 0, stream, wp, scales, biases, sdt, out, odt, R, K, gs);
+    else hipLaunchKernelGGL((dequant_kernel<8, false>), grid, block, 0, stream, wp, scales, biases, sdt, out, odt, R, K, gs);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_embedding(const void* ids, bool ids_signed, int64_t T, const void* w,
+                            const void* scales, const void* biases, int sdt, void* out, int odt,
+                            int64_t V, int64_t H, int gs, int bits, hipStream_t stream) {
+  const int64_t words = T * (H * bits / 32);
+  if (words == 0) return hipSuccess;
+  const bool vec = (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+  const dim3 grid(blocks_for(words, 256)), block(256);
+  const uint32_t* wp = static_cast<const uint32_t*>(w);
+  const int sg = ids_signed ? 1 : 0;
+  if (bits == 4) {
+    if (vec) hipLaunchKernelGGL((embedding_kernel<4, true>), grid, block, 0, stream, ids, sg, T, wp, scales, biases, sdt, out, odt, V, H, gs);
+    else hipLaunchKernelGGL((embedding_kernel<4, false>), grid, block, 0, stream, ids, sg, T, wp, scales, biases, sdt, out, odt, V, H, gs);
+  } else {
+    if (vec) hipLaunchKernelGGL((embedding_kernel<8, true>), grid, block, 0, stream, ids, sg, T, wp, scales, biases, sdt, out, odt, V, H, gs);
+    else hipLaunchKernelGGL((embedding_kernel<8, false>), grid, block, 0, stream, ids, sg, T, wp, scales, biases, sdt, out, odt, V, H, gs);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_take(const void* a, int64_t V, int64_t row_bytes, const void* ids,
+                       bool ids_signed, int64_t T, void* out, hipStream_t stream) {
+  if (T == 0 || row_bytes == 0) return hipSuccess;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(out);
+  const int sg = ids_signed ? 1 : 0;
+  const dim3 block(256);
+  if (row_bytes % 16 == 0 && al % 16 == 0) {
+    const int64_t units = row_bytes / 16;
+    hipLaunchKernelGGL(take_kernel<u32x4>, dim3(blocks_for(T * units, 256)), block, 0, stream,
+                       static_cast<const u32x4*>(a), V, units, ids, sg, T, static_cast<u32x4*>(out));
+  } else if (row_bytes % 4 == 0 && al % 4 == 0) {
+    const int64_t units = row_bytes / 4;
+    hipLaunchKernelGGL(take_kernel<uint32_t>, dim3(blocks_for(T * units, 256)), block, 0, stream,
+                       static_cast<const uint32_t*>(a), V, units, ids, sg, T, static_cast<uint32_t*>(out));
+  } else {
+    hipLaunchKernelGGL(take_kernel<uint8_t>, dim3(blocks_for(T * row_bytes, 256)), block, 0, stream,
+                       static_cast<const uint8_t*>(a), V, row_bytes, ids, sg, T, static_cast<uint8_t*>(out));
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_qmm_generic(const QmvArgs& a, bool transpose) {
+  if (a.M == 0 || a.N == 0) return hipSuccess;
+  const dim3 grid(blocks_for(a.N, 256), a.M < 65535 ? a.M : 65535), block(256);
+  const uint32_t* wp = static_cast<const uint32_t*>(a.w);
+  if (a.bits == 4)
+    hipLaunchKernelGGL(qmm_generic_kernel<4>, grid, block, 0, a.stream, a.x, a.xdt, wp, a.scales,
+                       a.biases, a.sdt, a.out, a.odt, a.M, a.N, a.K, a.gs, transpose ? 1 : 0);
+  else
+    hipLaunchKernelGGL(qmm_generic_kernel<8>, grid, block, 0, a.stream, a.x, a.xdt, wp, a.scales,
+                       a.biases, a.sdt, a.out, a.odt, a.M, a.N, a.K, a.gs, transpose ? 1 : 0);
+  return hipGetLastError();
+}
+
+}  // namespace kh

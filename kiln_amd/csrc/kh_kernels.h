@@ -1,0 +1,49 @@
+// kh_kernels.h — host-side launcher interface between the C ABI and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kh {
+
+// Quantized matmul, transpose=true: x [M, K], w [N, K*bits/32],
+// scales/biases [N, K/gs], out [M, N].
+struct QmvArgs {
+  const void* x;
+  int xdt;
+  const void* w;
+  const void* scales;
+  const void* biases;
+  int sdt;
+  void* out;
+  int odt;
+  int M, N, K, gs, bits;
+  hipStream_t stream;
+};
+
+// Decode path (M <= 64), MFMA on unscaled codes with per-group fp32 scaling.
+hipError_t launch_qmv(const QmvArgs& a);
+int qmv_waves(int N, int K, int gs);
+
+// Prefill path (any M; chosen for M > 64): LDS-tiled MFMA GEMM. `xsum` is a
+// device workspace of at least M * (K / gs) floats.
+hipError_t launch_qmm(const QmvArgs& a, float* xsum);
+
+// Any dtype / alignment / transpose: one thread per output, fp32 fma chain.
+hipError_t launch_qmm_generic(const QmvArgs& a, bool transpose);
+
+// Dequantize rows: w [R, K*bits/32] -> out [R, K].
+hipError_t launch_dequantize(const void* w, const void* scales, const void* biases, int sdt,
+                             void* out, int odt, int64_t R, int64_t K, int gs, int bits,
+                             hipStream_t stream);
+
+// Quantized embedding: out[t, :] = dequantize(row ids[t]); V table rows.
+hipError_t launch_embedding(const void* ids, bool ids_signed, int64_t T, const void* w,
+                            const void* scales, const void* biases, int sdt, void* out, int odt,
+                            int64_t V, int64_t H, int gs, int bits, hipStream_t stream);
+
+// take(a, ids, axis=0) on rows of row_bytes bytes.
+hipError_t launch_take(const void* a, int64_t V, int64_t row_bytes, const void* ids,
+                       bool ids_signed, int64_t T, void* out, hipStream_t stream);
+
+}  // namespace kh

@@ -1,0 +1,367 @@
+// kiln_hip.hip — the extern "C" boundary (include/kiln_hip.h): argument
+// validation, MLX-compatible shape rules, thread-local error reporting, and
+// dispatch to the gfx950 kernels.
+//
+// Error behaviour mirrors the Kiln/mlx-c contract (crates/kiln-mlx/src/error.rs:24-72):
+// a failing call returns non-zero and leaves a message retrievable on the
+// calling thread; nothing aborts. Every argument check runs before any HIP
+// call, so validation behaves identically on a machine without a GPU.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "../../include/kiln_hip.h"
+#include "kh_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+const char* dtype_name(int dt) {
+  switch (dt) {
+    case KH_BOOL: return "bool";
+    case KH_UINT8: return "uint8";
+    case KH_UINT16: return "uint16";
+    case KH_UINT32: return "uint32";
+    case KH_UINT64: return "uint64";
+    case KH_INT8: return "int8";
+    case KH_INT16: return "int16";
+    case KH_INT32: return "int32";
+    case KH_INT64: return "int64";
+    case KH_FLOAT16: return "float16";
+    case KH_FLOAT32: return "float32";
+    case KH_FLOAT64: return "float64";
+    case KH_BFLOAT16: return "bfloat16";
+    case KH_COMPLEX64: return "complex64";
+    default: return "unknown";
+  }
+}
+
+int64_t dtype_size(int dt) {
+  switch (dt) {
+    case KH_BOOL: case KH_UINT8: case KH_INT8: return 1;
+    case KH_UINT16: case KH_INT16: case KH_FLOAT16: case KH_BFLOAT16: return 2;
+    case KH_UINT32: case KH_INT32: case KH_FLOAT32: return 4;
+    case KH_UINT64: case KH_INT64: case KH_FLOAT64: case KH_COMPLEX64: return 8;
+    default: return 0;
+  }
+}
+
+bool is_float(int dt) { return dt == KH_FLOAT16 || dt == KH_BFLOAT16 || dt == KH_FLOAT32; }
+
+std::string shape_str(const kh_array* a) {
+  std::string s = "(";
+  for (int i = 0; i < a->ndim; ++i) {
+    if (i) s += ",";
+    s += std::to_string(a->shape[i]);
+  }
+  return s + ")";
+}
+
+int64_t numel(const kh_array* a) {
+  int64_t n = 1;
+  for (int i = 0; i < a->ndim; ++i) n *= a->shape[i];
+  return n;
+}
+
+// Structural checks shared by every entry point.
+int check_array(const kh_array* a, const char* op, const char* name) {
+  if (!a) return fail(KH_ERR_INVALID_ARGUMENT, "[%s] %s is NULL", op, name);
+  if (a->ndim < 0 || a->ndim > KH_MAX_NDIM)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] %s has ndim %d (0..%d)", op, name, a->ndim, KH_MAX_NDIM);
+  if (dtype_size(a->dtype) == 0)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] %s has invalid dtype %d", op, name, a->dtype);
+  for (int i = 0; i < a->ndim; ++i)
+    if (a->shape[i] < 0)
+      return fail(KH_ERR_INVALID_ARGUMENT, "[%s] %s has negative dimension %lld", op, name,
+                  (long long)a->shape[i]);
+  if (!a->data && numel(a) > 0) return fail(KH_ERR_INVALID_ARGUMENT, "[%s] %s data is NULL", op, name);
+  return KH_OK;
+}
+
+// Quantization parameters: the domain Kiln accepts
+// (crates/kiln-models/src/config.rs:137-148, 735-760) with MLX's defaults.
+int check_quant(const char* op, kh_optional_int gs_opt, kh_optional_int bits_opt, const char* mode,
+                int* gs, int* bits) {
+  if (mode && std::strcmp(mode, "affine") != 0)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] quantization mode \"%s\" (supported: \"affine\")", op, mode);
+  *gs = gs_opt.has_value ? gs_opt.value : 64;
+  *bits = bits_opt.has_value ? bits_opt.value : 4;
+  if ((*bits != 4 && *bits != 8) || (*gs != 32 && *gs != 64 && *gs != 128))
+    return fail(KH_ERR_INVALID_ARGUMENT,
+                "[%s] bits=%d group_size=%d (supported: 4/8 bits, 32/64/128 groups)", op, *bits, *gs);
+  return KH_OK;
+}
+
+// Packed weights plus scales/biases of matching shape: w [..., R, C*bits/32]
+// with scales/biases [..., R, C/gs].
+int check_packed(const char* op, const kh_array* w, const kh_array* s, const kh_array* b, int gs,
+                 int bits, int64_t* rows, int64_t* cols) {
+  int rc;
+  if ((rc = check_array(w, op, "w")) || (rc = check_array(s, op, "scales")) ||
+      (rc = check_array(b, op, "biases")))
+    return rc;
+  if (w->dtype != KH_UINT32)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] packed weights must be uint32, got %s", op, dtype_name(w->dtype));
+  if (w->ndim < 2) return fail(KH_ERR_INVALID_ARGUMENT, "[%s] w must have ndim >= 2, got %d", op, w->ndim);
+  if (!is_float(s->dtype))
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] scales must be float16/bfloat16/float32, got %s", op, dtype_name(s->dtype));
+  if (s->dtype != b->dtype)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] scales (%s) and biases (%s) must share a dtype", op,
+                dtype_name(s->dtype), dtype_name(b->dtype));
+  if (s->ndim != w->ndim || b->ndim != w->ndim)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] w %s, scales %s, biases %s: ranks differ", op,
+                shape_str(w).c_str(), shape_str(s).c_str(), shape_str(b).c_str());
+  for (int i = 0; i < w->ndim; ++i)
+    if (s->shape[i] != b->shape[i])
+      return fail(KH_ERR_INVALID_ARGUMENT, "[%s] scales %s and biases %s differ in shape", op,
+                  shape_str(s).c_str(), shape_str(b).c_str());
+  for (int i = 0; i < w->ndim - 1; ++i)
+    if (s->shape[i] != w->shape[i])
+      return fail(KH_ERR_INVALID_ARGUMENT, "[%s] w %s and scales %s disagree", op,
+                  shape_str(w).c_str(), shape_str(s).c_str());
+  const int64_t c = w->shape[w->ndim - 1] * (32 / bits);
+  if (s->shape[s->ndim - 1] * gs != c)
+    return fail(KH_ERR_INVALID_ARGUMENT,
+                "[%s] w %s holds %lld columns at %d bits but scales %s cover %lld at group_size %d",
+                op, shape_str(w).c_str(), (long long)c, bits, shape_str(s).c_str(),
+                (long long)(s->shape[s->ndim - 1] * gs), gs);
+  *cols = c;
+  int64_t r = 1;
+  for (int i = 0; i < w->ndim - 1; ++i) r *= w->shape[i];
+  *rows = r;
+  return KH_OK;
+}
+
+int check_result(const char* op, const kh_array* res, const kh_array& want) {
+  int rc = check_array(res, op, "res");
+  if (rc) return rc;
+  if (!is_float(res->dtype))
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] res dtype must be float16/bfloat16/float32, got %s", op,
+                dtype_name(res->dtype));
+  bool same = res->ndim == want.ndim;
+  for (int i = 0; same && i < want.ndim; ++i) same = res->shape[i] == want.shape[i];
+  if (!same)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] res has shape %s, expected %s", op,
+                shape_str(res).c_str(), shape_str(&want).c_str());
+  return KH_OK;
+}
+
+int hip_fail(const char* op, hipError_t e) {
+  return fail(KH_ERR_DEVICE, "[%s] HIP error %d: %s", op, (int)e, hipGetErrorString(e));
+}
+
+// One-time per device: the code objects are built for gfx950 only.
+int check_device(const char* op) {
+  static std::mutex mu;
+  static std::map<int, bool> ok;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(KH_ERR_NO_DEVICE, "[%s] no HIP device: %s", op, hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = ok.find(dev);
+  if (it == ok.end()) {
+    hipDeviceProp_t p;
+    e = hipGetDeviceProperties(&p, dev);
+    if (e != hipSuccess) return hip_fail(op, e);
+    it = ok.emplace(dev, std::strncmp(p.gcnArchName, "gfx950", 6) == 0).first;
+    if (!it->second)
+      return fail(KH_ERR_NO_DEVICE, "[%s] device %d is %s; this library is built for gfx950 only",
+                  op, dev, p.gcnArchName);
+  }
+  return it->second ? KH_OK : fail(KH_ERR_NO_DEVICE, "[%s] device %d is not gfx950", op, dev);
+}
+
+// Per (device, stream) float workspace for the prefill path's group sums.
+// Grown on demand (synchronising that stream first), never shrunk; steady
+// state performs no allocation.
+float* workspace(hipStream_t stream, size_t floats, int* rc, const char* op) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> pool;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  std::lock_guard<std::mutex> lock(mu);
+  auto& slot = pool[{dev, stream}];
+  const size_t bytes = floats * sizeof(float);
+  if (slot.second < bytes) {
+    hipError_t e = hipStreamSynchronize(stream);
+    if (e == hipSuccess && slot.first) e = hipFree(slot.first);
+    slot = {nullptr, 0};
+    void* p = nullptr;
+    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+    if (e == hipSuccess) e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+      *rc = hip_fail(op, e);
+      return nullptr;
+    }
+    slot = {p, want};
+  }
+  *rc = KH_OK;
+  return static_cast<float*>(slot.first);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* kh_last_error(void) { return g_last_error.c_str(); }
+
+const char* kh_version(void) { return "kiln-hip 0.1.0 (gfx950)"; }
+
+int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
+                        const kh_array* scales, const kh_array* biases, bool transpose,
+                        kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,
+                        kh_stream stream) {
+  const char* op = "quantized_matmul";
+  int gs, bits, rc;
+  if ((rc = check_quant(op, group_size, bits_opt, mode, &gs, &bits))) return rc;
+  if ((rc = check_array(x, op, "x"))) return rc;
+  if (!is_float(x->dtype))
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] x must be float16/bfloat16/float32, got %s", op, dtype_name(x->dtype));
+  if (x->ndim < 1) return fail(KH_ERR_INVALID_ARGUMENT, "[%s] x must have ndim >= 1", op);
+  int64_t rows, cols;
+  if ((rc = check_packed(op, w, scales, biases, gs, bits, &rows, &cols))) return rc;
+  if (w->ndim != 2)
+    return fail(KH_ERR_UNSUPPORTED, "[%s] batched w %s is not supported (2-D weights only)", op,
+                shape_str(w).c_str());
+  const int64_t K = x->shape[x->ndim - 1];
+  const int64_t wK = transpose ? cols : w->shape[0];
+  const int64_t N = transpose ? w->shape[0] : cols;
+  if (wK != K)
+    return fail(KH_ERR_INVALID_ARGUMENT,
+                "[%s] x %s has %lld input features but w %s (transpose=%s) expects %lld", op,
+                shape_str(x).c_str(), (long long)K, shape_str(w).c_str(), transpose ? "true" : "false",
+                (long long)wK);
+  kh_array want = *x;
+  want.shape[want.ndim - 1] = N;
+  if ((rc = check_result(op, res, want))) return rc;
+  const int64_t M = K ? numel(x) / K : numel(res) / (N ? N : 1);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return fail(KH_ERR_UNSUPPORTED, "[%s] dimensions beyond 2^31 are not supported", op);
+  if (M == 0 || N == 0) return KH_OK;
+  if ((rc = check_device(op))) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (K == 0) {
+    hipError_t e = hipMemsetAsync(res->data, 0, (size_t)(M * N * dtype_size(res->dtype)), st);
+    return e == hipSuccess ? KH_OK : hip_fail(op, e);
+  }
+  kh::QmvArgs a{x->data, x->dtype, w->data, scales->data, biases->data, scales->dtype, res->data,
+                res->dtype, (int)M, (int)N, (int)K, gs, bits, st};
+  const bool fast = transpose && x->dtype != KH_FLOAT32 && aligned16(x->data) && aligned16(w->data);
+  hipError_t e;
+  if (!fast) {
+    e = kh::launch_qmm_generic(a, transpose);
+  } else if (M <= 64) {
+    e = kh::launch_qmv(a);
+  } else {
+    float* ws = workspace(st, (size_t)M * (size_t)(K / gs), &rc, op);
+    if (!ws) return rc;
+    e = kh::launch_qmm(a, ws);
+  }
+  return e == hipSuccess ? KH_OK : hip_fail(op, e);
+}
+
+int kh_dequantize(kh_array* res, const kh_array* w, const kh_array* scales, const kh_array* biases,
+                  kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,
+                  kh_stream stream) {
+  const char* op = "dequantize";
+  int gs, bits, rc;
+  if ((rc = check_quant(op, group_size, bits_opt, mode, &gs, &bits))) return rc;
+  int64_t rows, cols;
+  if ((rc = check_packed(op, w, scales, biases, gs, bits, &rows, &cols))) return rc;
+  kh_array want = *w;
+  want.shape[want.ndim - 1] = cols;
+  if ((rc = check_result(op, res, want))) return rc;
+  if (rows == 0 || cols == 0) return KH_OK;
+  if ((rc = check_device(op))) return rc;
+  hipError_t e = kh::launch_dequantize(w->data, scales->data, biases->data, scales->dtype, res->data,
+                                       res->dtype, rows, cols, gs, bits, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? KH_OK : hip_fail(op, e);
+}
+
+int kh_take(kh_array* res, const kh_array* a, const kh_array* indices, kh_stream stream) {
+  const char* op = "take";
+  int rc;
+  if ((rc = check_array(a, op, "a")) || (rc = check_array(indices, op, "indices")) ||
+      (rc = check_array(res, op, "res")))
+    return rc;
+  if (a->ndim < 1) return fail(KH_ERR_INVALID_ARGUMENT, "[%s] cannot take along axis 0 of a scalar", op);
+  if (indices->dtype != KH_UINT32 && indices->dtype != KH_INT32)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] indices must be uint32 or int32, got %s", op, dtype_name(indices->dtype));
+  if (indices->ndim + a->ndim - 1 > KH_MAX_NDIM)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] result rank exceeds %d", op, KH_MAX_NDIM);
+  kh_array want{};
+  want.dtype = a->dtype;
+  want.ndim = indices->ndim + a->ndim - 1;
+  for (int i = 0; i < indices->ndim; ++i) want.shape[i] = indices->shape[i];
+  for (int i = 1; i < a->ndim; ++i) want.shape[indices->ndim + i - 1] = a->shape[i];
+  if (res->dtype != a->dtype)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] res dtype %s differs from a dtype %s", op,
+                dtype_name(res->dtype), dtype_name(a->dtype));
+  bool same = res->ndim == want.ndim;
+  for (int i = 0; same && i < want.ndim; ++i) same = res->shape[i] == want.shape[i];
+  if (!same)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] res has shape %s, expected %s", op,
+                shape_str(res).c_str(), shape_str(&want).c_str());
+  const int64_t T = numel(indices);
+  const int64_t V = a->shape[0];
+  int64_t row = dtype_size(a->dtype);
+  for (int i = 1; i < a->ndim; ++i) row *= a->shape[i];
+  if (T == 0 || row == 0) return KH_OK;
+  if (V == 0) return fail(KH_ERR_INVALID_ARGUMENT, "[%s] cannot take from an empty axis", op);
+  if ((rc = check_device(op))) return rc;
+  hipError_t e = kh::launch_take(a->data, V, row, indices->data, indices->dtype == KH_INT32, T,
+                                 res->data, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? KH_OK : hip_fail(op, e);
+}
+
+int kh_quantized_embedding(kh_array* res, const kh_array* ids, const kh_array* w,
+                           const kh_array* scales, const kh_array* biases,
+                           kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,
+                           kh_stream stream) {
+  const char* op = "quantized_embedding";
+  int gs, bits, rc;
+  if ((rc = check_quant(op, group_size, bits_opt, mode, &gs, &bits))) return rc;
+  if ((rc = check_array(ids, op, "ids"))) return rc;
+  if (ids->dtype != KH_UINT32 && ids->dtype != KH_INT32)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] ids must be uint32 or int32, got %s", op, dtype_name(ids->dtype));
+  int64_t rows, cols;
+  if ((rc = check_packed(op, w, scales, biases, gs, bits, &rows, &cols))) return rc;
+  if (w->ndim != 2)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] embedding table must be 2-D, got %s", op, shape_str(w).c_str());
+  if (ids->ndim + 1 > KH_MAX_NDIM)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] result rank exceeds %d", op, KH_MAX_NDIM);
+  kh_array want{};
+  want.ndim = ids->ndim + 1;
+  for (int i = 0; i < ids->ndim; ++i) want.shape[i] = ids->shape[i];
+  want.shape[ids->ndim] = cols;
+  if ((rc = check_result(op, res, want))) return rc;
+  const int64_t T = numel(ids);
+  if (T == 0 || cols == 0) return KH_OK;
+  if (w->shape[0] == 0) return fail(KH_ERR_INVALID_ARGUMENT, "[%s] empty embedding table", op);
+  if ((rc = check_device(op))) return rc;
+  hipError_t e = kh::launch_embedding(ids->data, ids->dtype == KH_INT32, T, w->data, scales->data,
+                                      biases->data, scales->dtype, res->data, res->dtype,
+                                      w->shape[0], cols, gs, bits, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? KH_OK : hip_fail(op, e);
+}
+
+}  // extern "C"

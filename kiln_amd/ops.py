@@ -1,0 +1,154 @@
+"""Host-side mirror of `kiln_mlx::ops` for the quantized path, over libkiln_hip.
+
+Same names, argument order and meaning as the reference wrappers
+(crates/kiln-mlx/src/ops.rs):
+
+    quantized_matmul(x, w, scales, biases, transpose, group_size, bits)  ops.rs:359-388
+    dequantize(w, scales, biases, group_size, bits)                      ops.rs:456-484
+    take(a, indices, axis)                                                ops.rs:249-254
+
+plus `quantized_embedding`, the fused take+dequantize of Embedding::lookup
+(crates/kiln-models/src/nn.rs:159-176). Failures raise `KilnError` carrying
+the library's message, as `check` turns mlx-c status codes into `MlxError`
+(crates/kiln-mlx/src/error.rs:62-72).
+
+Tensors are torch tensors resident on the GPU (torch is the device-memory and
+stream plumbing here). Work is enqueued on torch's current stream for the
+tensors' device, or on `stream` (a torch.cuda.Stream) when given; like MLX's
+lazy evaluation, results are ready once that stream is synchronised.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_TORCH_TO_KH = {
+    torch.bfloat16: _lib.BFLOAT16,
+    torch.float16: _lib.FLOAT16,
+    torch.float32: _lib.FLOAT32,
+    torch.uint32: _lib.UINT32,
+    torch.int32: _lib.INT32,
+    torch.uint8: _lib.UINT8,
+    torch.int8: _lib.INT8,
+    torch.int16: _lib.INT16,
+    torch.uint16: _lib.UINT16,
+    torch.int64: _lib.INT64,
+    torch.float64: _lib.FLOAT64,
+    torch.bool: _lib.BOOL,
+}
+
+_NAMES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+class KilnError(RuntimeError):
+    """A failing library call: `status` is the kh_status code."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+        self.message = message
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise KilnError(status, _lib.last_error() or _lib.STATUS.get(status, str(status)))
+
+
+def _desc(t: torch.Tensor, name: str, as_dtype: int | None = None) -> _lib.KhArray:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise KilnError(1, f"{name} must be a GPU tensor (got device {t.device}); "
+                           "libkiln_hip runs on gfx950 only")
+    if not t.is_contiguous():
+        raise KilnError(1, f"{name} must be row-contiguous")
+    dt = as_dtype if as_dtype is not None else _TORCH_TO_KH.get(t.dtype)
+    if dt is None:
+        raise KilnError(1, f"{name} has unsupported dtype {t.dtype}")
+    return _lib.array(t.data_ptr(), dt, t.shape)
+
+
+def _packed(w: torch.Tensor) -> _lib.KhArray:
+    # Packed weights are uint32; an int32 tensor holding the same bits is
+    # accepted and reinterpreted (torch has few uint32 kernels).
+    if w.dtype in (torch.uint32, torch.int32):
+        return _desc(w, "w", _lib.UINT32)
+    return _desc(w, "w")
+
+
+def _stream_handle(t: torch.Tensor, stream) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream(t.device)
+    return s.cuda_stream
+
+
+def result_dtype(x_dtype: torch.dtype, s_dtype: torch.dtype) -> torch.dtype:
+    """MLX type promotion over (x, scales, biases): equal float types stay,
+    bf16 with f16 (or anything with f32) promotes to float32."""
+    return x_dtype if x_dtype == s_dtype else torch.float32
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: torch.Tensor, transpose: bool = True, group_size: int = 64,
+                     bits: int = 4, *, mode: str = "affine", out_dtype=None,
+                     out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """`x @ dequantize(w, scales, biases)^T` (transpose) or `x @ dequantize(...)`."""
+    if isinstance(out_dtype, str):
+        out_dtype = _NAMES[out_dtype]
+    if transpose:
+        N = w.shape[0]
+    else:
+        N = w.shape[-1] * (32 // bits) if bits in (4, 8) else w.shape[-1]
+    if out is None:
+        od = out_dtype or result_dtype(x.dtype, scales.dtype)
+        out = torch.empty((*x.shape[:-1], N), dtype=od, device=x.device)
+    _check(_lib.lib().kh_quantized_matmul(
+        _desc(out, "res"), _desc(x, "x"), _packed(w), _desc(scales, "scales"),
+        _desc(biases, "biases"), bool(transpose), _lib.opt(group_size), _lib.opt(bits),
+        mode.encode() if mode is not None else None, _stream_handle(x, stream)))
+    return out
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               group_size: int = 64, bits: int = 4, *, mode: str = "affine", out_dtype=None,
+               out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Dense [..., K] values `scale*q + bias`; dtype defaults to the scales'."""
+    if isinstance(out_dtype, str):
+        out_dtype = _NAMES[out_dtype]
+    if out is None:
+        cols = w.shape[-1] * (32 // bits) if bits in (4, 8) else w.shape[-1]
+        out = torch.empty((*w.shape[:-1], cols), dtype=out_dtype or scales.dtype, device=w.device)
+    _check(_lib.lib().kh_dequantize(
+        _desc(out, "res"), _packed(w), _desc(scales, "scales"), _desc(biases, "biases"),
+        _lib.opt(group_size), _lib.opt(bits), mode.encode() if mode is not None else None,
+        _stream_handle(w, stream)))
+    return out
+
+
+def take(a: torch.Tensor, indices: torch.Tensor, axis: int = 0, *,
+         out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Rows of `a` at `indices` along axis 0 (the embedding-lookup form)."""
+    if axis != 0:
+        raise KilnError(2, f"take along axis {axis} is not supported (axis 0 only)")
+    if out is None:
+        out = torch.empty((*indices.shape, *a.shape[1:]), dtype=a.dtype, device=a.device)
+    _check(_lib.lib().kh_take(_desc(out, "res"), _desc(a, "a"), _desc(indices, "indices"),
+                              _stream_handle(a, stream)))
+    return out
+
+
+def quantized_embedding(ids: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                        biases: torch.Tensor, group_size: int = 64, bits: int = 4, *,
+                        mode: str = "affine", out_dtype=None, out: torch.Tensor | None = None,
+                        stream=None) -> torch.Tensor:
+    """dequantize(take(w, ids), take(scales, ids), take(biases, ids)) in one pass."""
+    if isinstance(out_dtype, str):
+        out_dtype = _NAMES[out_dtype]
+    if out is None:
+        cols = w.shape[-1] * (32 // bits) if bits in (4, 8) else w.shape[-1]
+        out = torch.empty((*ids.shape, cols), dtype=out_dtype or scales.dtype, device=w.device)
+    _check(_lib.lib().kh_quantized_embedding(
+        _desc(out, "res"), _desc(ids, "ids"), _packed(w), _desc(scales, "scales"),
+        _desc(biases, "biases"), _lib.opt(group_size), _lib.opt(bits),
+        mode.encode() if mode is not None else None, _stream_handle(w, stream)))
+    return out

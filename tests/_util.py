@@ -1,0 +1,37 @@
+"""Helpers shared by the GPU tests: numpy bit patterns <-> device tensors and
+the parity metrics."""
+import numpy as np
+import torch
+
+TORCH_DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def dev(a: np.ndarray, dt: str | None = None) -> torch.Tensor:
+    """numpy -> cuda tensor; uint16 arrays are reinterpreted as dt (bf16/f16),
+    uint32 as int32 bits."""
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).view(TORCH_DT[dt]).cuda()
+    if a.dtype == np.uint32:
+        return torch.from_numpy(a.view(np.int32)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    """cuda tensor -> numpy bit patterns (uint16 for 16-bit floats)."""
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.int32:
+        return t.numpy().view(np.uint32)
+    return t.numpy()
+
+
+def parity_metrics(y: np.ndarray, ref: np.ndarray):
+    """(max|err| / max|ref|, mean|err| / mean|ref|) — the matmul tolerance:
+    max|err| <= 2e-2 * max|ref| and mean relative error <= 1e-3, with both
+    arrays as float64 values of the same output dtype."""
+    y = y.astype(np.float64)
+    ref = ref.astype(np.float64)
+    err = np.abs(y - ref)
+    return float(err.max() / max(np.abs(ref).max(), 1e-30)), float(err.mean() / max(np.abs(ref).mean(), 1e-30))

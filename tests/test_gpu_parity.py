@@ -1,0 +1,208 @@
+"""GPU parity: libkiln_hip (through the C ABI via kiln_amd.ops) against the
+CPU oracle on the same seeded inputs.
+
+Bars: unpack/dequantize/embedding/take are bit-exact; quantized_matmul meets
+max|err| <= 2e-2 * max|ref| and mean|err| / mean|ref| <= 1e-3 against the
+oracle's float32-accumulated result rounded to the same output dtype, and a
+much tighter elementwise bound on float32 outputs that catches any layout
+slip (a wrong code, group or scale costs far more than it allows).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from kiln_amd import ops
+from kiln_amd.workloads import make_linear_numpy, make_x_numpy
+
+from _util import dev, host, parity_metrics
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+MAX_TOL, MEAN_TOL = 2e-2, 1e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def _case(M, N, K, gs, bits, xdt="bf16", sdt="f16", seed=0):
+    L = make_linear_numpy(N, K, gs, "q4" if bits == 4 else "q8", seed=seed, sdt=sdt)
+    x = make_x_numpy(M, K, seed=seed + 100, xdt=xdt)
+    return L, x
+
+
+def _run(L, x, gs, bits, xdt, sdt, odt, transpose=True):
+    y = ops.quantized_matmul(dev(x, xdt), dev(L["w"]), dev(L["scales"], sdt), dev(L["biases"], sdt),
+                             transpose, gs, bits, out_dtype=odt)
+    torch.cuda.synchronize()
+    return host(y)
+
+
+def _check_f32(oracle, L, x, gs, bits, xdt, sdt, y, transpose=True, rel=3e-5):
+    ref = oracle.quantized_matmul_f32(x, xdt, L["w"], L["scales"], L["biases"], sdt, gs, bits, transpose)
+    W = oracle.to_f32(oracle.dequantize(L["w"], L["scales"], L["biases"], sdt, gs, bits, "f32"), "f32")
+    mag = np.abs(oracle.to_f32(x, xdt)).astype(np.float64) @ np.abs(W.T if transpose else W).astype(np.float64)
+    bad = np.abs(y.astype(np.float64) - ref) > rel * mag + 1e-30
+    assert not bad.any(), f"{bad.sum()} elements off; first at {np.argwhere(bad)[0]}"
+    return ref
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 64, 65, 200])
+def test_qmm_bf16_f32out(oracle, bits, gs, M):
+    print(f"case qmm bits={bits} gs={gs} M={M}", flush=True)
+    N, K = 80, 512
+    L, x = _case(M, N, K, gs, bits, seed=M + bits + gs)
+    y = _run(L, x, gs, bits, "bf16", "f16", "f32")
+    _check_f32(oracle, L, x, gs, bits, "bf16", "f16", y)
+
+
+@pytest.mark.parametrize("xdt,sdt,odt", [("bf16", "bf16", "bf16"), ("f16", "f16", "f16"),
+                                         ("bf16", "f16", "bf16"), ("f16", "bf16", "f32"),
+                                         ("bf16", "f32", "f32")])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [1, 7, 96])
+def test_qmm_dtypes_tolerance(oracle, xdt, sdt, odt, bits, M):
+    print(f"case qmm dtypes x={xdt} s={sdt} o={odt} bits={bits} M={M}", flush=True)
+    gs, N, K = 64, 144, 384
+    L, x = _case(M, N, K, gs, bits, xdt=xdt, sdt=sdt, seed=5)
+    y = _run(L, x, gs, bits, xdt, sdt, odt)
+    ref = oracle.quantized_matmul(x, xdt, L["w"], L["scales"], L["biases"], sdt, gs, bits, True, odt)
+    mx, mean = parity_metrics(oracle.to_f32(y, odt), oracle.to_f32(ref, odt))
+    assert mx <= MAX_TOL and mean <= MEAN_TOL, (mx, mean)
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 64), (8, 32)])
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+def test_qmm_transpose_false(oracle, bits, gs, xdt):
+    print(f"case qmm transpose=false bits={bits} gs={gs} x={xdt}", flush=True)
+    M, N, K = 5, 128, 192
+    L = make_linear_numpy(K, N, gs, "q4" if bits == 4 else "q8", seed=3)
+    x = make_x_numpy(M, K, seed=4, xdt=xdt)
+    y = _run(L, x, gs, bits, xdt, "f16", "f32", transpose=False)
+    ref = oracle.quantized_matmul_f32(x, xdt, L["w"], L["scales"], L["biases"], "f16", gs, bits, False)
+    # the general kernel performs the oracle's exact float32 operation sequence
+    assert np.array_equal(y, ref)
+
+
+def test_qmm_f32_activations_bit_exact(oracle):
+    M, N, K, gs = 3, 40, 256, 32
+    L, x = _case(M, N, K, gs, 4, xdt="f32", seed=9)
+    y = _run(L, x, gs, 4, "f32", "f16", "f32")
+    assert np.array_equal(y, oracle.quantized_matmul_f32(x, "f32", L["w"], L["scales"], L["biases"], "f16", gs, 4))
+
+
+def test_qmm_leading_dims_and_empty(oracle):
+    L, x = _case(6, 32, 128, 64, 4, seed=1)
+    x3 = x.reshape(2, 3, 128)
+    y = ops.quantized_matmul(dev(x3, "bf16"), dev(L["w"]), dev(L["scales"], "f16"),
+                             dev(L["biases"], "f16"), True, 64, 4, out_dtype="f32")
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (2, 3, 32)
+    flat = _run(L, x, 64, 4, "bf16", "f16", "f32")
+    assert np.array_equal(host(y).reshape(6, 32), flat)
+    e = ops.quantized_matmul(torch.empty((0, 128), dtype=torch.bfloat16, device="cuda"),
+                             dev(L["w"]), dev(L["scales"], "f16"), dev(L["biases"], "f16"), True, 64, 4)
+    assert tuple(e.shape) == (0, 32)
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 64), (8, 128), (4, 32)])
+def test_rows_are_m_invariant_on_decode_path(bits, gs):
+    """Row r of the result is bitwise the same for every M <= 64 (the property
+    Kiln's calibration probes, crates/kiln-models/src/nn.rs:301-327)."""
+    N, K = 272, 1024
+    L, x = _case(64, N, K, gs, bits, seed=21)
+    full = _run(L, x, gs, bits, "bf16", "f16", "bf16")
+    for M in (1, 2, 5, 16, 17, 33, 63):
+        part = _run(L, x[:M], gs, bits, "bf16", "f16", "bf16")
+        assert np.array_equal(part, full[:M]), M
+
+
+@pytest.mark.parametrize("path", sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz")))
+def test_golden_fixtures(path):
+    f = np.load(os.path.join(GOLDEN, path))
+    bits, gs, sdt = int(f["bits"]), int(f["gs"]), str(f["sdt"])
+    w, s, b = dev(f["w"]), dev(f["scales"], sdt), dev(f["biases"], sdt)
+    d32 = host(ops.dequantize(w, s, b, gs, bits, out_dtype="f32"))
+    db = host(ops.dequantize(w, s, b, gs, bits, out_dtype="bf16"))
+    emb = host(ops.quantized_embedding(dev(f["ids"]).view(torch.int32), w, s, b, gs, bits, out_dtype="bf16"))
+    y = host(ops.quantized_matmul(dev(f["x"], "bf16"), w, s, b, True, gs, bits, out_dtype="f32"))
+    torch.cuda.synchronize()
+    assert np.array_equal(d32.view(np.uint32), f["deq_f32"])
+    assert np.array_equal(db, f["deq_bf16"])
+    assert np.array_equal(emb, f["emb_bf16"])
+    y_exact = f["y_f32"].view(np.float32).astype(np.float64)
+    mag = np.abs((f["x"].astype(np.uint32) << 16).view(np.float32)).astype(np.float64) @ \
+        np.abs(f["deq_f32"].view(np.float32)).T.astype(np.float64)
+    assert np.all(np.abs(y - y_exact) <= 3e-5 * mag)
+
+
+@pytest.mark.parametrize("bits,gs,sdt,odt", [(4, 64, "f16", "bf16"), (8, 32, "bf16", "bf16"),
+                                             (4, 128, "f32", "f32"), (8, 64, "f16", "f16")])
+def test_dequantize_bit_exact(oracle, bits, gs, sdt, odt):
+    L = make_linear_numpy(333, 1024, gs, "q4" if bits == 4 else "q8", seed=2, sdt=sdt)
+    got = host(ops.dequantize(dev(L["w"]), dev(L["scales"], sdt), dev(L["biases"], sdt), gs, bits,
+                              out_dtype=odt))
+    want = oracle.dequantize(L["w"], L["scales"], L["biases"], sdt, gs, bits, odt)
+    assert np.array_equal(got, want)
+
+
+def test_dequantize_default_dtype_is_scales_dtype():
+    L = make_linear_numpy(4, 64, 32, "q4", sdt="bf16")
+    y = ops.dequantize(dev(L["w"]), dev(L["scales"], "bf16"), dev(L["biases"], "bf16"), 32, 4)
+    assert y.dtype == torch.bfloat16
+
+
+def test_embedding_full_table_zipf_bit_exact(oracle):
+    """Config 4(a): tied 4-bit gs128 table [128256, 4096], 4096 Zipf(1.1) ids."""
+    from kiln_amd.workloads import make_linear_device
+    V, H, gs = 128256, 4096, 128
+    T = make_linear_device(V, H, gs, "emb", seed=44)
+    rng = np.random.default_rng(45)
+    ids = np.minimum(rng.zipf(1.1, 4096) - 1, V - 1).astype(np.uint32)
+    got = host(ops.quantized_embedding(dev(ids), T["w"], T["scales"],
+                                       T["biases"], gs, 4, out_dtype="bf16"))
+    # the oracle needs only the rows it gathers
+    uniq, inv = np.unique(ids, return_inverse=True)
+    sel = torch.from_numpy(uniq.astype(np.int64)).cuda()
+    w = host(T["w"][sel])
+    s = host(T["scales"][sel])
+    b = host(T["biases"][sel])
+    want = oracle.embedding(inv.astype(np.uint32), w, s, b, "f16", gs, 4, "bf16")
+    assert np.array_equal(got, want)
+
+
+def test_embedding_signed_ids_and_out_of_range():
+    L = make_linear_numpy(50, 256, 64, "emb", seed=3)
+    w, s, b = dev(L["w"]), dev(L["scales"], "f16"), dev(L["biases"], "f16")
+    ids = torch.tensor([[-1, 0, 49], [50, -51, 7]], dtype=torch.int32, device="cuda")
+    y = host(ops.quantized_embedding(ids, w, s, b, 64, 4, out_dtype="f32"))
+    full = host(ops.dequantize(w, s, b, 64, 4, out_dtype="f32"))
+    assert np.array_equal(y[0, 0], full[49]) and np.array_equal(y[0, 2], full[49])
+    assert np.array_equal(y[0, 1], full[0]) and np.array_equal(y[1, 2], full[7])
+    assert not y[1, 0].any() and not y[1, 1].any()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.int32, torch.uint8])
+def test_take_rows(dtype):
+    a = (torch.arange(10 * 6, device="cuda") % 251).to(dtype).reshape(10, 6)
+    idx = torch.tensor([3, 0, 9, 3], dtype=torch.int32, device="cuda")
+    got = ops.take(a, idx, 0)
+    assert torch.equal(got, a[idx.long()])
+    b = torch.arange(8 * 4 * 4, device="cuda", dtype=torch.float32).reshape(8, 4, 4)
+    idx2 = torch.tensor([[1, 7], [0, 2]], dtype=torch.int32, device="cuda")
+    assert torch.equal(ops.take(b, idx2), b[idx2.long()])
+
+
+def test_errors_raise_kiln_error():
+    L, x = _case(1, 32, 128, 64, 4)
+    with pytest.raises(ops.KilnError) as e:
+        ops.quantized_matmul(dev(x, "bf16"), dev(L["w"]), dev(L["scales"], "f16"),
+                             dev(L["biases"], "f16"), True, 64, 3)
+    assert e.value.status == 1 and "bits=3" in str(e.value)

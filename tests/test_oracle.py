@@ -1,0 +1,216 @@
+"""Pins the CPU oracle (oracle/) before anything is compared against it.
+
+Each function of the oracle is checked against something that does not share
+its code: hand-built known-answer words, the exact-rational golden fixtures
+(tests/golden/make_golden.py), numpy/torch conversions, closed-form special
+cases, and an independent numpy float64 restatement.
+"""
+import glob
+import os
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# --------------------------------------------------------------------------- unpack / pack
+
+def test_unpack_known_words(oracle):
+    w = np.array([[0x76543210, 0xFEDCBA98]], dtype=np.uint32)
+    assert oracle.unpack(w, 4).tolist() == [list(range(16))]
+    w8 = np.array([[0x03020100, 0xFFFEFDFC]], dtype=np.uint32)
+    assert oracle.unpack(w8, 8).tolist() == [[0, 1, 2, 3, 252, 253, 254, 255]]
+    assert oracle.unpack(np.full((1, 1), 0xFFFFFFFF, np.uint32), 4).tolist() == [[15] * 8]
+    assert oracle.unpack(np.zeros((1, 1), np.uint32), 8).tolist() == [[0] * 4]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_unpack_one_hot_column_order(oracle, bits):
+    per = 32 // bits
+    for j in range(per):
+        w = np.array([[1 << (bits * j)]], dtype=np.uint32)
+        expect = [0] * per
+        expect[j] = 1
+        assert oracle.unpack(w, bits).tolist() == [expect]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_pack_unpack_roundtrip_and_numpy(oracle, bits):
+    rng = np.random.default_rng(bits)
+    codes = rng.integers(0, 1 << bits, (13, 96), dtype=np.uint8)
+    w = oracle.pack(codes, bits)
+    assert np.array_equal(w, oracle.np_pack(codes, bits))
+    assert np.array_equal(oracle.unpack(w, bits), codes)
+    assert np.array_equal(oracle.np_unpack(w, bits), codes)
+
+
+# --------------------------------------------------------------------------- rounding
+
+def _sweep_f32():
+    rng = np.random.default_rng(7)
+    vals = [0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, 1e-8, 6.1035156e-05, 6.0e-05,
+            5.96e-08, 2.98e-08, 3.0e-08, np.inf, -np.inf, 3.4e38, 1.0000001, 1.00390625,
+            1.005859375, 1.001953125]
+    r = rng.standard_normal(4000).astype(np.float32) * (10.0 ** rng.integers(-9, 6, 4000))
+    # exact bf16 ties: low half 0x8000
+    ties = (rng.integers(0, 2 ** 16, 200).astype(np.uint32) << 16 | 0x8000).view(np.float32)
+    return np.concatenate([np.array(vals, np.float32), r.astype(np.float32),
+                           ties[np.isfinite(ties)]]).astype(np.float32)
+
+
+def test_bf16_rounding_matches_torch(oracle):
+    v = _sweep_f32()
+    c = np.array([oracle.lib().kho_f32_to_bf16(float(f)) for f in v], dtype=np.uint16)
+    t = torch.from_numpy(v).bfloat16().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(c, t)
+    assert np.array_equal(oracle.from_f32(v, "bf16"), t)
+
+
+def test_f16_rounding_matches_numpy(oracle):
+    v = _sweep_f32()
+    c = np.array([oracle.lib().kho_f32_to_f16(float(f)) for f in v], dtype=np.uint16)
+    n = v.astype(np.float16).view(np.uint16)
+    assert np.array_equal(c, n)
+    back = np.array([oracle.lib().kho_f16_to_f32(int(h)) for h in n[:500]], dtype=np.float32)
+    assert np.array_equal(back, n[:500].view(np.float16).astype(np.float32))
+
+
+# --------------------------------------------------------------------------- dequantize
+
+@pytest.mark.parametrize("sdt", ["f16", "bf16"])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequant_special_cases(oracle, sdt, bits):
+    half = 1 << (bits - 1)
+    s = oracle.from_f32(np.array([[0.0125, 0.0, 0.01]], np.float32), sdt)
+    sv = oracle.to_f32(s, sdt)
+    b = oracle.from_f32(np.array([[-half * sv[0, 0], 0.75, -half * sv[0, 2]]], np.float32), sdt)
+    bv = oracle.to_f32(b, sdt)
+    per = 32 // bits
+    codes = np.zeros((1, 96), np.uint8)
+    codes[0, 0:32] = np.arange(32) % (1 << bits)
+    codes[0, 32:64] = (1 << bits) - 1
+    codes[0, 64:96] = half
+    w = oracle.np_pack(codes, bits)
+    d = oracle.to_f32(oracle.dequantize(w, s, b, sdt, 32, bits, "f32"), "f32")
+    assert d[0, 0] == bv[0, 0]                           # q = 0 -> bias
+    assert np.all(d[0, 32:64] == bv[0, 1])               # scale 0 -> bias broadcast
+    assert np.all(d[0, 64:96] == 0.0)                    # q = zero point, b = -half*s -> 0
+    assert per in (4, 8)
+
+
+@pytest.mark.parametrize("sdt", ["f16", "bf16"])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequant_every_code_against_exact(oracle, sdt, bits):
+    rng = np.random.default_rng(3)
+    K, gs = 256 * (bits // 4), 32
+    codes = np.tile(np.arange(1 << bits, dtype=np.uint8), 40 * K // (1 << bits))[: 40 * K].reshape(40, K)
+    s = oracle.from_f32(rng.uniform(-0.05, 0.05, (40, K // gs)).astype(np.float32), sdt)
+    b = oracle.from_f32(rng.uniform(-2, 2, (40, K // gs)).astype(np.float32), sdt)
+    w = oracle.np_pack(codes, bits)
+    exact = oracle.np_dequantize_f64(w, s, b, sdt, gs, bits)
+    for odt in ("f32", "bf16", "f16"):
+        got = oracle.dequantize(w, s, b, sdt, gs, bits, odt)
+        want = oracle.from_f32(exact.astype(np.float32), odt) if odt != "bf16" else \
+            torch.from_numpy(exact.astype(np.float32)).bfloat16().view(torch.int16).numpy().view(np.uint16)
+        # `exact` holds scale*q + bias without rounding (f64 has room for it), so
+        # exact -> f32 is the single rounding of the fma; narrower outputs round
+        # that f32 value once more, which is the dequantisation rule.
+        assert np.array_equal(got, want), odt
+
+
+def test_dequant_f32_scales_is_single_fma(oracle):
+    rng = np.random.default_rng(5)
+    s = rng.uniform(-1, 1, (3, 2)).astype(np.float32)
+    b = rng.uniform(-1, 1, (3, 2)).astype(np.float32)
+    codes = rng.integers(0, 16, (3, 64), dtype=np.uint8)
+    got = oracle.dequantize(oracle.np_pack(codes, 4), s, b, "f32", 32, 4, "f32")
+    for r in range(3):
+        for k in range(64):
+            exact = Fraction(float(s[r, k // 32])) * int(codes[r, k]) + Fraction(float(b[r, k // 32]))
+            assert got[r, k] == np.float32(float(exact)) or \
+                abs(Fraction(float(got[r, k])) - exact) <= abs(exact) * Fraction(1, 2 ** 24)
+
+
+# --------------------------------------------------------------------------- golden fixtures
+
+def _fixtures():
+    return sorted(glob.glob(os.path.join(GOLDEN, "*.npz")))
+
+
+@pytest.mark.parametrize("path", _fixtures(), ids=os.path.basename)
+def test_oracle_against_golden(oracle, path):
+    f = np.load(path)
+    bits, gs, sdt = int(f["bits"]), int(f["gs"]), str(f["sdt"])
+    assert np.array_equal(oracle.unpack(f["w"], bits), f["codes"])
+    deq = oracle.dequantize(f["w"], f["scales"], f["biases"], sdt, gs, bits, "f32")
+    assert np.array_equal(deq.view(np.uint32), f["deq_f32"])
+    deqb = oracle.dequantize(f["w"], f["scales"], f["biases"], sdt, gs, bits, "bf16")
+    assert np.array_equal(deqb, f["deq_bf16"])
+    emb = oracle.embedding(f["ids"], f["w"], f["scales"], f["biases"], sdt, gs, bits, "bf16")
+    assert np.array_equal(emb, f["emb_bf16"])
+    y = oracle.quantized_matmul_f32(f["x"], "bf16", f["w"], f["scales"], f["biases"], sdt, gs, bits)
+    y_exact = f["y_f32"].view(np.float32)
+    scale = np.abs(oracle.to_f32(f["x"], "bf16")) @ np.abs(deq).T
+    assert np.all(np.abs(y - y_exact) <= 1e-6 * scale + 1e-30)
+    yb = oracle.from_f32(y, "bf16").astype(np.int32)
+    assert np.max(np.abs(yb - f["y_bf16"].astype(np.int32))) <= 1
+
+
+# --------------------------------------------------------------------------- matmul
+
+@pytest.mark.parametrize("transpose", [True, False])
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (8, 128)])
+def test_qmm_c_vs_numpy_f64(oracle, transpose, bits, gs):
+    from kiln_amd.workloads import make_linear_numpy, make_x_numpy
+    M, N, K = 5, 128, 256
+    if transpose:
+        L = make_linear_numpy(N, K, gs, "q4" if bits == 4 else "q8", seed=11)
+    else:
+        L = make_linear_numpy(K, N, gs, "q4" if bits == 4 else "q8", seed=11)
+    x = make_x_numpy(M, K, seed=2)
+    y = oracle.quantized_matmul_f32(x, "bf16", L["w"], L["scales"], L["biases"], "f16", gs, bits,
+                                    transpose)
+    ref = oracle.np_qmm_f64(x, "bf16", L["w"], L["scales"], L["biases"], "f16", gs, bits, transpose)
+    W = oracle.np_dequantize_f64(L["w"], L["scales"], L["biases"], "f16", gs, bits)
+    mag = np.abs(oracle.to_f32(x, "bf16")).astype(np.float64) @ np.abs(W.T if transpose else W)
+    assert np.all(np.abs(y - ref) <= 2e-6 * mag)
+
+
+def test_qmm_linearity_and_row_independence(oracle):
+    from kiln_amd.workloads import make_linear_numpy, make_x_numpy
+    L = make_linear_numpy(48, 128, 64, "q4", seed=4)
+    x = make_x_numpy(6, 128, seed=9)
+    full = oracle.quantized_matmul_f32(x, "bf16", L["w"], L["scales"], L["biases"], "f16", 64, 4)
+    for m in range(6):
+        one = oracle.quantized_matmul_f32(x[m:m + 1], "bf16", L["w"], L["scales"], L["biases"], "f16", 64, 4)
+        assert np.array_equal(one[0], full[m])
+    # y(2x) == 2 y(x) exactly (power-of-two scaling commutes with rounding)
+    x2 = oracle.from_f32(2 * oracle.to_f32(x, "bf16"), "bf16")
+    y2 = oracle.quantized_matmul_f32(x2, "bf16", L["w"], L["scales"], L["biases"], "f16", 64, 4)
+    assert np.array_equal(y2, 2 * full)
+
+
+# --------------------------------------------------------------------------- take / embedding
+
+def test_embedding_equals_take_then_dequantize(oracle):
+    from kiln_amd.workloads import make_linear_numpy
+    L = make_linear_numpy(300, 256, 128, "emb", seed=8)
+    ids = np.array([[0, 299, 17], [17, 5, 250]], dtype=np.uint32)
+    emb = oracle.embedding(ids, L["w"], L["scales"], L["biases"], "f16", 128, 4, "bf16")
+    w, s, b = oracle.take(L["w"], ids), oracle.take(L["scales"], ids), oracle.take(L["biases"], ids)
+    assert np.array_equal(emb, oracle.dequantize(w, s, b, "f16", 128, 4, "bf16"))
+    assert np.array_equal(w, L["w"][ids.astype(np.int64)])
+
+
+def test_take_out_of_range_and_negative(oracle):
+    a = np.arange(40, dtype=np.uint32).reshape(10, 4)
+    ids = np.array([-1, 3, 10, -11, 0], dtype=np.int32)
+    got = oracle.take(a, ids)
+    assert got[0].tolist() == a[9].tolist()
+    assert got[1].tolist() == a[3].tolist()
+    assert got[2].tolist() == [0, 0, 0, 0]
+    assert got[3].tolist() == [0, 0, 0, 0]
+    assert got[4].tolist() == a[0].tolist()
