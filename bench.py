@@ -77,48 +77,71 @@ def main():
     outs = {name: torch.empty((1, N), dtype=torch.bfloat16, device=dev) for name, N, _ in shapes}
     stream = torch.cuda.current_stream(dev)
 
-    def step(i, events=None):
+    def step(i):
         L = layers[i % copies]
         for name, N, K in shapes:
             W = L[name]
-            if events is not None:
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
             ops.quantized_matmul(xs[K], W["w"], W["scales"], W["biases"], True, gs, bits,
-                                 out=outs[name], stream=stream)
-            if events is not None:
-                e1.record(stream)
-                events.append((name, e0, e1))
+                                 out=outs[name])
 
-    for i in range(args.warmup):
+    def capture(fn):
+        """Record fn's launches (made on torch's current stream, which is the
+        capture stream inside the context) into a HIP graph."""
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        return graph
+
+    # Eager warm-up, then one graph holding `copies` decode steps (one per
+    # weight copy) so a replay walks > 512 MB of distinct weights.
+    for i in range(copies):
         step(i)
+    torch.cuda.synchronize()
+    g_step = capture(lambda: [step(i) for i in range(copies)])
+    reps = max(1, -(-args.steps // copies))
+    wreps = max(1, -(-args.warmup // copies))
+    for _ in range(wreps):
+        g_step.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
+    for _ in range(reps):
+        g_step.replay()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_per_step = wall * 1e3 / args.steps
+    nsteps = reps * copies
+    ms_per_step = wall * 1e3 / nsteps
     step_bytes = sum(layer_bytes(N, K, 1, bits, gs) for _, N, K in shapes)
-    value = step_bytes / (wall / args.steps) / 1e9
+    value = step_bytes / (wall / nsteps) / 1e9
 
-    # Per-launch durations (HIP events on the library's stream), separate pass.
-    events = []
-    for i in range(min(args.steps, 100)):
-        step(i, events)
-    torch.cuda.synchronize()
-    per_shape = {}
-    for name, e0, e1 in events:
-        per_shape.setdefault(name, []).append(e0.elapsed_time(e1))
+    # Per-launch duration of each shape: a graph of that shape's launches over
+    # every weight copy, bracketed by HIP events recorded on the replay stream.
+    stream = torch.cuda.current_stream(dev)
+    per_shape_us = {}
+    for name, N, K in shapes:
+        def one_shape(name=name, K=K):
+            for i in range(copies):
+                W = layers[i][name]
+                ops.quantized_matmul(xs[K], W["w"], W["scales"], W["biases"], True, gs, bits,
+                                     out=outs[name])
+        gr = capture(one_shape)
+        gr.replay()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        nrep = 20
+        e0.record(stream)
+        for _ in range(nrep):
+            gr.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        per_shape_us[name] = 1e3 * e0.elapsed_time(e1) / (nrep * copies)
     dom = "gate"
     dN, dK = next((N, K) for n, N, K in shapes if n == dom)
-    dom_us = 1e3 * sum(per_shape[dom]) / len(per_shape[dom])
+    dom_us = per_shape_us[dom]
     dom_bytes = layer_bytes(dN, dK, 1, bits, gs)
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
-    per_shape_gbs = {n: round(layer_bytes(N, K, 1, bits, gs) / (1e-3 * sum(per_shape[n]) / len(per_shape[n])) / 1e9, 1)
+    per_shape_gbs = {n: round(layer_bytes(N, K, 1, bits, gs) / (per_shape_us[n] * 1e-6) / 1e9, 1)
                      for n, N, K in shapes}
-    per_shape_us = {n: round(1e3 * sum(v) / len(v), 2) for n, v in per_shape.items()}
+    per_shape_us = {n: round(v, 2) for n, v in per_shape_us.items()}
 
     # Prefill: the seven linears at M = prefill_m, MFMA dequant-GEMM path.
     Mp = args.prefill_m
@@ -134,7 +157,7 @@ def main():
                 e1 = torch.cuda.Event(enable_timing=True)
                 e0.record(stream)
             ops.quantized_matmul(xp[K], W["w"], W["scales"], W["biases"], True, gs, bits,
-                                 out=op[name], stream=stream)
+                                 out=op[name])
             if events is not None:
                 e1.record(stream)
                 events.append((name, e0, e1))
@@ -172,7 +195,7 @@ def main():
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": nsteps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,

@@ -43,6 +43,14 @@ def lib() -> ctypes.CDLL:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(
                 f"{LIB_PATH} is missing: build the HIP library first (python -m kiln_amd.build)")
+        # One HIP runtime per process: torch ships its own libamdhip64 (same
+        # soname, libamdhip64.so.7) and loads it under the name
+        # "libamdhip64.so". Loading torch first lets this library's
+        # dependency resolve to that already-loaded copy; loading this library
+        # first would pull in /opt/rocm's copy and torch would then load a
+        # second runtime beside it.
+        import torch  # noqa: F401
+
         L = ctypes.CDLL(LIB_PATH)
         P = ctypes.POINTER(KhArray)
         L.kh_quantized_matmul.argtypes = [P, P, P, P, P, ctypes.c_bool, KhOptionalInt,

@@ -150,9 +150,21 @@ __global__ void qmm_generic_kernel(const void* __restrict__ x, int xdt,
   }
 }
 
+__global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 inline unsigned blocks_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
 }  // namespace
+
+hipError_t launch_fill_u32(void* p, int64_t n, uint32_t value, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream,
+                     static_cast<uint32_t*>(p), n, value);
+  return hipGetLastError();
+}
 
 hipError_t launch_dequantize(const void* w, const void* scales, const void* biases, int sdt,
                              void* out, int odt, int64_t R, int64_t K, int gs, int bits,

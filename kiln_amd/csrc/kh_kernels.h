@@ -23,7 +23,9 @@ struct QmvArgs {
 
 // Decode path (M <= 64), MFMA on unscaled codes with per-group fp32 scaling.
 hipError_t launch_qmv(const QmvArgs& a);
-int qmv_waves(int N, int K, int gs);
+
+// Set n 32-bit words to value (a kernel, so it is safe inside graph capture).
+hipError_t launch_fill_u32(void* p, int64_t n, uint32_t value, hipStream_t stream);
 
 // Prefill path (any M; chosen for M > 64): LDS-tiled MFMA GEMM. `xsum` is a
 // device workspace of at least M * (K / gs) floats.

@@ -8,23 +8,41 @@
 // weight is ever rounded:
 //   y[m, n] = sum_g  s[n,g] * P'[m,n,g] + (b[n,g] - OFF*s[n,g]) * X[m,g]
 //   P'[m,n,g] = sum_{k in g} x[m,k] * (OFF + q[n,k])      (MFMA, fp32 accumulate)
-//   X[m,g]    = sum_{k in g} x[m,k]                        (MFMA against ones)
+//   X[m,g]    = sum_{k in g} x[m,k]                        (fp32, computed once per workgroup)
 // OFF + q is exactly representable in the MFMA input type: it is built by
 // OR-ing the code into the mantissa of OFF (bf16: OFF = 128, 7-bit mantissa;
 // f16: OFF = 1024, 10-bit mantissa), except 8-bit codes with bf16 activations,
 // which go through an exact int->float conversion with OFF = 0.
 //
-// Work decomposition: one workgroup owns 16 output rows (one MFMA column
-// tile) and all M <= 64 activation rows (MT m-tiles of 16). Its NWK waves
-// split the K groups into contiguous ranges and reduce their fp32 partials
-// through LDS in fixed wave order, so every output's summation order depends
-// only on (N, K, group_size, bits) — never on M or on scheduling.
+// Work decomposition. One workgroup owns one 16-row output tile (the MFMA
+// column dimension) and all M <= 64 activation rows. Its W waves split the
+// row's code blocks into W contiguous ranges. A block is 16 bytes per lane:
+// the four lane groups of a wave read 4 consecutive words each, 64 contiguous
+// bytes per output row per load instruction (128 codes at 4 bits, 64 at 8).
+// MFMA step j of a block takes word j (4-bit) or words 2j, 2j+1 (8-bit) from
+// every lane group.
 //
-// MFMA v_mfma_f32_16x16x32_{bf16,f16}: A = activations (16 m x 32 k),
+// When a block spans NC > 1 quantization groups (4-bit gs32/gs64, 8-bit
+// gs32), lane groups of different groups must not share an accumulator. Each
+// group ("chain") is given its own D rows instead: activation rows are packed
+// as (chain, m) into the 16 MFMA rows, and the A operand of a row is the
+// activation for lane groups of that row's chain and zero for the others
+// (zero lanes read a zero area of LDS). At M = 1 one MFMA per step serves
+// every chain; larger M uses more row tiles. Each D element sees the same
+// inputs whatever the tiling, so results do not depend on M.
+//
+// Per workgroup the activations of the current windows are staged in LDS,
+// permuted into the MFMA pair order, with the per-group sums X and the
+// scales/biases of the tile's rows (converted to fp32, bias pre-offset). The
+// first chunk of code loads is issued before staging so both overlap. Final
+// sums: for every output, chains in ascending order, and within a chain the
+// W wave partials in wave order. W depends only on (N, K, group_size, bits),
+// so every output's summation order is independent of M: row r of the result
+// is bitwise identical for every M <= 64.
+//
+// MFMA v_mfma_f32_16x16x32_{bf16,f16}: A = activations (16 rows x 32 k),
 // B = codes (32 k x 16 n). Lane l supplies row/column l%16 and the eight k of
-// block l/16; D lane l holds column l%16, rows 4*(l/16)+0..3. Per step the
-// four lane groups read four different words of the same group, so a group
-// (gs/32 steps) is reduced inside one accumulator chain.
+// block l/16; D lane l holds column l%16, rows 4*(l/16)+0..3.
 #include "kh_common.h"
 #include "kh_kernels.h"
 
@@ -50,29 +68,19 @@ __device__ __forceinline__ u32x4 permute_x(u32x4 d) {
   return r;
 }
 
-template <bool XBF16>
-struct MagicT;
-template <>
-struct MagicT<true> {  // bf16: 0x4300 = 128.0
-  static constexpr uint32_t magic = 0x43004300u;
-  static constexpr uint32_t ones = 0x3f803f80u;
-};
-template <>
-struct MagicT<false> {  // f16: 0x6400 = 1024.0
-  static constexpr uint32_t magic = 0x64006400u;
-  static constexpr uint32_t ones = 0x3c003c00u;
-};
-
 template <int BITS, bool XBF16>
 struct CodeOffset {
   static constexpr float value = (BITS == 8 && XBF16) ? 0.0f : (XBF16 ? 128.0f : 1024.0f);
 };
 
 // Eight codes (one 4-bit word, or two 8-bit words) -> B operand, values OFF + q.
+// `mag` is the OFF bit pattern (bf16 0x4300 = 128.0, f16 0x6400 = 1024.0 in
+// both halves) held in a VGPR, so each (mask, or) pair becomes one
+// v_and_or_b32 (a VOP3 may carry only one non-VGPR constant).
 template <int BITS, bool XBF16>
-__device__ __forceinline__ u32x4 codes_to_b(const uint32_t* q) {
+__device__ __forceinline__ u32x4 codes_to_b(const uint32_t* q, uint32_t mag) {
   u32x4 r;
-  constexpr uint32_t MAG = MagicT<XBF16>::magic;
+  const uint32_t MAG = mag;
   if constexpr (BITS == 4) {
     const uint32_t u = q[0];
     r[0] = (u & 0x000f000fu) | MAG;
@@ -111,175 +119,367 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-constexpr int QMV_MAX_WAVES = 16;
+template <bool SBF16>
+__device__ __forceinline__ float half_to_f32(uint32_t h) {
+  return SBF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
 
-template <int BITS, int GS, bool XBF16, int MT>
-__global__ __launch_bounds__(1024) void qmv_kernel(const uint16_t* __restrict__ x,
-                                                   const uint32_t* __restrict__ w,
-                                                   const void* __restrict__ scales,
-                                                   const void* __restrict__ biases, int sdt,
-                                                   void* __restrict__ out, int odt, int M, int N,
-                                                   int K) {
-  constexpr int CPW = 32 / BITS;   // codes per word
-  constexpr int S = GS / 32;       // MFMA k-steps per group
-  constexpr int WPS = 8 / CPW;     // words per lane per step
-  constexpr int LW = S * WPS;      // words per lane per group
-  constexpr int WPG = GS / CPW;    // words per group per row (= 4 * LW)
+#ifndef KH_QMV_NT
+#define KH_QMV_NT 0
+#endif
+// Weight-stream load (plain, or non-temporal when KH_QMV_NT is set).
+template <typename T>
+__device__ __forceinline__ T ldw(const T* p) {
+#if KH_QMV_NT
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+
+#ifndef KH_QMV_INFLIGHT
+#define KH_QMV_INFLIGHT 32  // VGPRs per lane for one chunk of code loads
+#endif
+#ifndef KH_QMV_WAVE_TARGET
+#define KH_QMV_WAVE_TARGET 8192  // waves per launch to aim for
+#endif
+#ifndef KH_QMV_MAX_WAVES
+#define KH_QMV_MAX_WAVES 8
+#endif
+#ifndef KH_QMV_LDS
+#define KH_QMV_LDS 49152  // LDS bytes per workgroup for staged activations
+#endif
+
+constexpr int pow2_floor(int v) {
+  int p = 1;
+  while (p * 2 <= v) p *= 2;
+  return p;
+}
+
+// Geometry shared by host and device.
+template <int BITS, int GS>
+struct QmvGeom {
+  static constexpr int CPW = 32 / BITS;         // codes per word
+  static constexpr int CB = 16 * CPW;           // codes per block (per output row)
+  static constexpr int SPB = CB / 32;           // MFMA steps per block
+  static constexpr int WPS = 8 / CPW;           // words per step per lane
+  static constexpr int KBB = CB / 8;            // 8-element k-blocks per block
+  static constexpr int NC = CB >= GS ? CB / GS : 1;   // groups (chains) per block
+  static constexpr int BPG = GS > CB ? GS / CB : 1;   // blocks per group
+  static constexpr int LGC = 4 / NC;            // lane groups per chain
+  static constexpr int U = KH_QMV_INFLIGHT / 4; // blocks per load chunk
+};
+
+struct QmvPlan {
+  int waves;   // K-split waves per workgroup
+  int nct;     // chains per row tile
+  int mt;      // activation rows per chain in a tile (16 / nct)
+  int tiles;   // row tiles
+  int wu;      // units (BPG blocks) per wave staged per round
+  int batch;   // waves staged together (divides waves)
+  size_t lds;  // dynamic LDS bytes
+};
+
+static int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+template <int BITS, int GS>
+static QmvPlan plan_qmv_t(int M, int N, int K) {
+  using Gm = QmvGeom<BITS, GS>;
+  const int NB = ceil_div(K, Gm::CB);
+  const int NU = NB / Gm::BPG;
+  const int tiles16 = ceil_div(N, 16);
+  int waves = 1;
+  while (waves < KH_QMV_MAX_WAVES && tiles16 * waves * 2 <= KH_QMV_WAVE_TARGET && NU / (waves * 2) >= 2)
+    waves *= 2;
+  int nct = 1;
+  if (M <= 16) nct = pow2_floor(16 / M) < Gm::NC ? pow2_floor(16 / M) : Gm::NC;
+  const int mt = 16 / nct;
+  int mtiles = 1;  // m tiles, rounded up to a power of two (extra tiles see only rows >= M)
+  while (mtiles < ceil_div(M, mt)) mtiles *= 2;
+  const int tiles = (Gm::NC / nct) * mtiles;
+  // LDS per staged unit: activations, group sums (D-row layout), scale/bias pairs.
+  const size_t per_unit = (size_t)Gm::BPG * Gm::CB * M * 2 + (size_t)tiles * 16 * 4 + 16 * Gm::NC * 8;
+  int batch = waves;
+  while (batch > 1 && per_unit * batch > KH_QMV_LDS) batch /= 2;
+  int wu = (int)(KH_QMV_LDS / (per_unit * batch));
+  if (wu < 1) wu = 1;
+  if (wu > ceil_div(NU, waves)) wu = ceil_div(NU, waves);
+  size_t lds = (size_t)batch * wu * per_unit + (size_t)Gm::SPB * M * 16;
+  const size_t red = (size_t)waves * 64 * 16 + (size_t)M * 16 * 4;
+  if (red > lds) lds = red;
+  return {waves, nct, mt, tiles, wu, batch, lds};
+}
+
+template <int BITS, int GS, bool XBF16, bool SBF16, int TILES>
+__global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    void* __restrict__ out, int odt, int M, int N, int K, int nct, int wu, int batch) {
+  using Gm = QmvGeom<BITS, GS>;
+  constexpr int CB = Gm::CB, SPB = Gm::SPB, WPS = Gm::WPS, KBB = Gm::KBB;
+  constexpr int NC = Gm::NC, BPG = Gm::BPG, LGC = Gm::LGC, U = Gm::U;
   constexpr float OFF = CodeOffset<BITS, XBF16>::value;
 
-  __shared__ f32x4 red[QMV_MAX_WAVES * MT * 64];
+  extern __shared__ __align__(16) unsigned char smem[];
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int nwk = blockDim.x >> 6;
+  const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
+  const int W = nthreads >> 6;
+  const int lw2 = __builtin_ctz(W);
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15;
   const int lg = lane >> 4;
   const int n = blockIdx.x * 16 + col;
   const bool nvalid = n < N;
+  const int nc = nvalid ? n : N - 1;  // clamped: every weight load is in bounds
   const int G = K / GS;
-  const int64_t WR = K / CPW;
-  const int g0 = (int)((int64_t)G * wave / nwk);
-  const int g1 = (int)((int64_t)G * (wave + 1) / nwk);
+  const int WR = K / Gm::CPW;                    // words per row
+  const int NB = (K + CB - 1) / CB;              // blocks per row (last may be partial)
+  const int NU = NB / BPG;                       // units per row
+  const int mt = 16 / nct;                       // rows per chain in a tile
+  const int cgroups = NC / nct;                  // chain groups (tiles per m range)
 
-  const uint32_t* wrow = w + (int64_t)(nvalid ? n : 0) * WR + lg * LW;
-  const int64_t sbase = (int64_t)(nvalid ? n : 0) * G;
+  // LDS carve-up for one staging step: [batch][wu] units of
+  //   xs  : BPG*KBB*M u32x4  permuted activations,
+  //   xd  : TILES*16 floats   group sums in D-row layout,
+  //   sb  : 16*NC float2      (scale, bias - OFF*scale) per tile row and chain,
+  // followed by the zero area (SPB*M u32x4).
+  const int xs_u = BPG * KBB * M;                // u32x4 per unit
+  u32x4* xs = reinterpret_cast<u32x4*>(smem);
+  float* xd = reinterpret_cast<float*>(xs + (size_t)batch * wu * xs_u);
+  float2* sb = reinterpret_cast<float2*>(xd + (size_t)batch * wu * TILES * 16);
+  u32x4* zero = reinterpret_cast<u32x4*>(sb + (size_t)batch * wu * 16 * NC);
 
-  u32x4 ones;
-  ones[0] = ones[1] = ones[2] = ones[3] = MagicT<XBF16>::ones;
+  // Units of each wave: [(NU*v) >> lw2, (NU*(v+1)) >> lw2).
+  const int r0 = (NU * wave) >> lw2;
+  const int r1 = (NU * (wave + 1)) >> lw2;
+  const int longest = (NU + W - 1) >> lw2;
 
-  f32x4 acc[MT];
+  // Lane roles per tile: row r = col of the A operand; the lane's D rows are
+  // 4*lg .. 4*lg+3, all of one chain because mt is a multiple of 4.
+  int a_off[TILES];   // u32x4 offset of this lane's A operand inside a block (-1: zero lane)
+  int d_chain[TILES]; // chain of this lane's D rows
 #pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < TILES; ++t) {
+    const int cg = t % cgroups, mtile = t / cgroups;
+    const int ca = cg * nct + col / mt, ma = mtile * mt + col % mt;  // chain and row of A row `col`
+    const bool live = (lg / LGC) == ca && ma < M;
+    // k-block of lane group lg, step j, inside a block: lg*SPB + j
+    a_off[t] = live ? (lg * SPB) * M + ma : -1;
+    d_chain[t] = cg * nct + (4 * lg) / mt;
+  }
 
-  for (int g = g0; g < g1; ++g) {
-    uint32_t q[LW];
-    if (nvalid) {
-      const uint32_t* src = wrow + (int64_t)g * WPG;
-      if constexpr (LW == 1) {
-        q[0] = __builtin_nontemporal_load(src);
-      } else if constexpr (LW == 2) {
-        u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src));
-        q[0] = v[0];
-        q[1] = v[1];
-      } else {
+  const uint32_t* wrow = w + (int64_t)nc * WR;
+  uint32_t mag = XBF16 ? 0x43004300u : 0x64006400u;
+  asm volatile("" : "+v"(mag));  // keep it in a VGPR (see codes_to_b)
+
+  f32x4 acc[TILES];
 #pragma unroll
-        for (int i = 0; i < LW; i += 4) {
-          u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + i));
-          q[i] = v[0];
-          q[i + 1] = v[1];
-          q[i + 2] = v[2];
-          q[i + 3] = v[3];
+  for (int t = 0; t < TILES; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int i = tid; i < SPB * M; i += nthreads) zero[i] = u32x4{0u, 0u, 0u, 0u};
+
+  const int nbatch = W / batch;
+  for (int step = 0; step < ((longest + wu - 1) / wu) * nbatch; ++step) {
+    const int off = (step / nbatch) * wu;      // unit offset within every wave's range
+    const int b0 = (step % nbatch) * batch;    // first wave staged in this step
+    const bool mine = wave >= b0 && wave < b0 + batch;
+    const int my_units = mine ? min(wu, r1 - (r0 + off)) : 0;
+    const int my_blocks = my_units * BPG;
+    // ---- first chunk of code loads, issued before staging
+    uint32_t q[U][4];
+    auto load_chunk = [&](int c0) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int blk = (r0 + off) * BPG + min(c0 + u, max(my_blocks - 1, 0));
+        // a lane chunk past the row end (partial last block) reads the row's
+        // last chunk instead; its activations are zero
+        const int word = min(blk * 16 + lg * 4, WR - 4);
+        const u32x4 v = ldw(reinterpret_cast<const u32x4*>(wrow + word));
+        q[u][0] = v[0];
+        q[u][1] = v[1];
+        q[u][2] = v[2];
+        q[u][3] = v[3];
+      }
+    };
+    if (my_blocks > 0) load_chunk(0);
+
+    // ---- stage activations, group sums, scales for the batch's units
+    __syncthreads();
+    {
+      const int items = batch * wu * BPG * KBB * M;
+      for (int it = tid; it < items; it += nthreads) {
+        const int m = it % M;
+        const int kb = (it / M) % (BPG * KBB);
+        const int ul = (it / (M * BPG * KBB)) % wu;
+        const int vb = it / (M * BPG * KBB * wu);
+        const int v = b0 + vb;
+        const int unit = ((NU * v) >> lw2) + off + ul;
+        const int vend = (NU * (v + 1)) >> lw2;
+        const int k = (unit * BPG * KBB + kb) * 8;
+        u32x4 val = u32x4{0u, 0u, 0u, 0u};
+        if (unit < vend && k < K)
+          val = permute_x<BITS>(*reinterpret_cast<const u32x4*>(x + (int64_t)m * K + k));
+        xs[(size_t)(vb * wu + ul) * xs_u + kb * M + m] = val;
+      }
+      const int sitems = batch * wu * 16 * NC;
+      for (int it = tid; it < sitems; it += nthreads) {
+        const int c = it % NC;
+        const int row = (it / NC) % 16;
+        const int ul = (it / (NC * 16)) % wu;
+        const int vb = it / (NC * 16 * wu);
+        const int v = b0 + vb;
+        const int unit = ((NU * v) >> lw2) + off + ul;
+        const int vend = (NU * (v + 1)) >> lw2;
+        const int g = unit * NC + c;
+        const int rn = min(blockIdx.x * 16 + row, N - 1);
+        float2 e = float2{0.f, 0.f};
+        if (unit < vend && g < G) {
+          const float sc = half_to_f32<SBF16>(scales[(int64_t)rn * G + g]);
+          e = float2{sc, fmaf(-OFF, sc, half_to_f32<SBF16>(biases[(int64_t)rn * G + g]))};
+        }
+        sb[(size_t)(vb * wu + ul) * 16 * NC + row * NC + c] = e;
+      }
+    }
+    __syncthreads();
+    {
+      // group sums in D-row layout: xd[(v*wu+ul)*TILES*16 + t*16 + r]
+      const int items = batch * wu * TILES * 16;
+      for (int it = tid; it < items; it += nthreads) {
+        const int r = it % 16;
+        const int t = (it / 16) % TILES;
+        const int vu = it / (16 * TILES);  // slot: vb*wu + ul
+        const int cg = t % cgroups, mtile = t / cgroups;
+        const int c = cg * nct + r / mt, m = mtile * mt + r % mt;
+        float sum = 0.f;
+        if (m < M) {
+          const u32x4* base = xs + (size_t)vu * xs_u;
+          for (int e = 0; e < GS / 8; ++e) {
+            const int kb = c * (GS / 8) + e;  // k-block within the unit
+            const u32x4 val = base[kb * M + m];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+              sum += XBF16 ? bf16_bits_to_f32(val[h] & 0xffffu) : f16_bits_to_f32(val[h] & 0xffffu);
+              sum += XBF16 ? bf16_bits_to_f32(val[h] >> 16) : f16_bits_to_f32(val[h] >> 16);
+            }
+          }
+        }
+        xd[it] = sum;
+      }
+    }
+    __syncthreads();
+
+    // ---- stream this wave's code blocks
+    const int slot = (wave - b0) * wu;
+    static_assert(BPG == 1 || TILES <= 4, "chains spanning blocks keep one D per tile");
+    f32x4 D[TILES];  // persists across the BPG blocks of a group
+    for (int c0 = 0; c0 < my_blocks; c0 += U) {
+      if (c0 > 0) load_chunk(c0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int b = c0 + u;
+        if (b >= my_blocks) continue;  // wave-uniform
+        const int ul = b / BPG, bib = b % BPG;
+        u32x4 B[SPB];
+#pragma unroll
+        for (int j = 0; j < SPB; ++j) B[j] = codes_to_b<BITS, XBF16>(&q[u][j * WPS], mag);
+        const u32x4* xunit = xs + (size_t)(slot + ul) * xs_u + bib * KBB * M;
+        const f32x4* xdu = reinterpret_cast<const f32x4*>(xd + (size_t)(slot + ul) * TILES * 16);
+        const float2* sbu = sb + (size_t)(slot + ul) * 16 * NC;
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) {
+          if (bib == 0) D[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+          const u32x4* ap = a_off[t] >= 0 ? xunit + a_off[t] : zero;
+#pragma unroll
+          for (int j = 0; j < SPB; ++j) D[t] = mfma<XBF16>(ap[j * M], B[j], D[t]);
+          if (bib == BPG - 1) {
+            const float2 e = sbu[col * NC + d_chain[t]];
+            const f32x4 X = xdu[t * 4 + lg];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              acc[t][i] = fmaf(e.x, D[t][i], acc[t][i]);
+              acc[t][i] = fmaf(e.y, X[i], acc[t][i]);
+            }
+          }
         }
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < LW; ++i) q[i] = 0;
     }
-    float sc = 0.f, bp = 0.f;
-    if (nvalid) {
-      sc = load_as_f32(scales, sdt, sbase + g);
-      bp = fmaf(-OFF, sc, load_as_f32(biases, sdt, sbase + g));
-    }
-
-    f32x4 P[MT], X[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      P[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-      X[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-      const u32x4 b = codes_to_b<BITS, XBF16>(q + j * WPS);
-      const int64_t kx = (int64_t)g * GS + 8 * (lg * S + j);
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const int m = t * 16 + col;
-        u32x4 a = u32x4{0u, 0u, 0u, 0u};
-        if (m < M) a = permute_x<BITS>(*reinterpret_cast<const u32x4*>(x + (int64_t)m * K + kx));
-        P[t] = mfma<XBF16>(a, b, P[t]);
-        X[t] = mfma<XBF16>(a, ones, X[t]);
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[t][i] = fmaf(sc, P[t][i], acc[t][i]);
-        acc[t][i] = fmaf(bp, X[t][i], acc[t][i]);
-      }
   }
 
-  if (nwk > 1) {
+  // ---- final sums: for each m-tile, chains ascending, waves in order
+  __syncthreads();
+  f32x4* red = reinterpret_cast<f32x4*>(smem);                      // [W][64]
+  float* outacc = reinterpret_cast<float*>(red + (size_t)W * 64);   // [M][16]
+  for (int i = tid; i < M * 16; i += nthreads) outacc[i] = 0.f;
 #pragma unroll
-    for (int t = 0; t < MT; ++t) red[(wave * MT + t) * 64 + lane] = acc[t];
+  for (int t = 0; t < TILES; ++t) {
     __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      f32x4 s = red[t * 64 + lane];
-      for (int v = 1; v < nwk; ++v) {
-        const f32x4 o = red[(v * MT + t) * 64 + lane];
-        s[0] += o[0];
-        s[1] += o[1];
-        s[2] += o[2];
-        s[3] += o[3];
+    red[wave * 64 + lane] = acc[t];
+    __syncthreads();
+    for (int it = tid; it < 256; it += nthreads) {
+      const int mtile = t / cgroups;
+      const int r_in = it / 16, nl = it % 16;  // (row within chain block, output column)
+      const int m = mtile * mt + r_in;
+      if (r_in < mt && m < M) {
+        float s = outacc[m * 16 + nl];
+        for (int cl = 0; cl < nct; ++cl) {
+          const int r = cl * mt + r_in;  // D row
+          const int ln = (r / 4) * 16 + nl, el = r % 4;
+          for (int v = 0; v < W; ++v) s += red[v * 64 + ln][el];
+        }
+        outacc[m * 16 + nl] = s;
       }
-      acc[t] = s;
     }
   }
-  if (!nvalid) return;
-#pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = t * 16 + 4 * lg + i;
-      if (m < M) store_from_f32(out, odt, (int64_t)m * N + n, acc[t][i]);
-    }
+  __syncthreads();
+  for (int i = tid; i < M * 16; i += nthreads) {
+    const int m = i / 16, nl = i % 16;
+    const int nn = blockIdx.x * 16 + nl;
+    if (nn < N) store_from_f32(out, odt, (int64_t)m * N + nn, outacc[i]);
+  }
 }
 
-// Waves per workgroup: enough waves in flight to cover the chip, at least two
-// groups per wave. Depends only on (N, K, group_size) so that the summation
-// order of an output row is the same for every M.
-int qmv_waves(int N, int K, int gs) {
-  const int tiles = (N + 15) / 16;
-  const int G = K / gs;
-  int nwk = 1;
-  while (nwk < QMV_MAX_WAVES && tiles * nwk < 8192 && G / (nwk * 2) >= 2) nwk *= 2;
-  return nwk;
-}
-
-template <int BITS, int GS, bool XBF16>
-static hipError_t launch_mt(const QmvArgs& a, int nwk) {
-  const dim3 grid((a.N + 15) / 16), block(64 * nwk);
-  const int mt = (a.M + 15) / 16;
-#define KH_QMV_LAUNCH(MTV)                                                                        \
-  hipLaunchKernelGGL((qmv_kernel<BITS, GS, XBF16, MTV>), grid, block, 0, a.stream,                \
-                     (const uint16_t*)a.x, (const uint32_t*)a.w, a.scales, a.biases, a.sdt, a.out, \
-                     a.odt, a.M, a.N, a.K)
-  switch (mt) {
+template <int BITS, int GS, bool XBF16, bool SBF16>
+static hipError_t launch_tiles(const QmvArgs& a) {
+  const QmvPlan p = plan_qmv_t<BITS, GS>(a.M, a.N, a.K);
+  const dim3 grid((a.N + 15) / 16), block(64 * p.waves);
+#define KH_QMV_LAUNCH(TV)                                                                       \
+  hipLaunchKernelGGL((qmv_kernel<BITS, GS, XBF16, SBF16, TV>), grid, block, p.lds, a.stream,   \
+                     (const uint16_t*)a.x, (const uint32_t*)a.w, (const uint16_t*)a.scales,    \
+                     (const uint16_t*)a.biases, a.out, a.odt, a.M, a.N, a.K, p.nct, p.wu, p.batch)
+  switch (p.tiles) {
     case 1: KH_QMV_LAUNCH(1); break;
     case 2: KH_QMV_LAUNCH(2); break;
-    case 3: KH_QMV_LAUNCH(3); break;
-    default: KH_QMV_LAUNCH(4); break;
+    case 4: KH_QMV_LAUNCH(4); break;
+    case 8: if constexpr (QmvGeom<BITS, GS>::BPG == 1) { KH_QMV_LAUNCH(8); break; } else return hipErrorInvalidValue;
+    case 16: if constexpr (QmvGeom<BITS, GS>::BPG == 1) { KH_QMV_LAUNCH(16); break; } else return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
   }
 #undef KH_QMV_LAUNCH
   return hipGetLastError();
 }
 
-template <int BITS, bool XBF16>
-static hipError_t launch_gs(const QmvArgs& a, int nwk) {
+template <int BITS, bool XBF16, bool SBF16>
+static hipError_t launch_gs(const QmvArgs& a) {
   switch (a.gs) {
-    case 32: return launch_mt<BITS, 32, XBF16>(a, nwk);
-    case 64: return launch_mt<BITS, 64, XBF16>(a, nwk);
-    default: return launch_mt<BITS, 128, XBF16>(a, nwk);
+    case 32: return launch_tiles<BITS, 32, XBF16, SBF16>(a);
+    case 64: return launch_tiles<BITS, 64, XBF16, SBF16>(a);
+    default: return launch_tiles<BITS, 128, XBF16, SBF16>(a);
   }
 }
 
+template <int BITS, bool XBF16>
+static hipError_t launch_st(const QmvArgs& a) {
+  return a.sdt == DT_BF16 ? launch_gs<BITS, XBF16, true>(a) : launch_gs<BITS, XBF16, false>(a);
+}
+
+// Scales and biases must be float16 or bfloat16 here (float32 scales take the
+// general kernel). Uses no device memory besides its arguments.
 hipError_t launch_qmv(const QmvArgs& a) {
-  const int nwk = qmv_waves(a.N, a.K, a.gs);
   const bool xbf16 = a.xdt == DT_BF16;
-  if (a.bits == 4) return xbf16 ? launch_gs<4, true>(a, nwk) : launch_gs<4, false>(a, nwk);
-  return xbf16 ? launch_gs<8, true>(a, nwk) : launch_gs<8, false>(a, nwk);
+  if (a.bits == 4) return xbf16 ? launch_st<4, true>(a) : launch_st<4, false>(a);
+  return xbf16 ? launch_st<8, true>(a) : launch_st<8, false>(a);
 }
 
 }  // namespace kh

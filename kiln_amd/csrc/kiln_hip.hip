@@ -15,6 +15,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "../../include/kiln_hip.h"
 #include "kh_kernels.h"
@@ -188,32 +189,70 @@ int check_device(const char* op) {
   return it->second ? KH_OK : fail(KH_ERR_NO_DEVICE, "[%s] device %d is not gfx950", op, dev);
 }
 
-// Per (device, stream) float workspace for the prefill path's group sums.
-// Grown on demand (synchronising that stream first), never shrunk; steady
-// state performs no allocation.
-float* workspace(hipStream_t stream, size_t floats, int* rc, const char* op) {
+// Per (device, stream) workspace: a counter region (kept all-zero between
+// calls: the split-K decode kernel returns every counter it takes to zero)
+// followed by float scratch (split-K partials, prefill group sums). Grown on
+// demand — synchronising that stream first — and never shrunk, so the steady
+// state performs no allocation. Calls on one stream are ordered, so they can
+// share it.
+constexpr size_t kCounterBytes = 64 * 1024;
+
+// Buffers replaced while their stream was capturing: a graph may still refer
+// to them, so they live until the process ends.
+std::vector<void*>& retired() {
+  static std::vector<void*> v;
+  return v;
+}
+
+struct Workspace {
+  unsigned* counters;
+  float* data;
+};
+
+bool workspace(hipStream_t stream, size_t floats, Workspace* ws, int* rc, const char* op) {
   static std::mutex mu;
   static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> pool;
   int dev = 0;
   (void)hipGetDevice(&dev);
   std::lock_guard<std::mutex> lock(mu);
   auto& slot = pool[{dev, stream}];
-  const size_t bytes = floats * sizeof(float);
+  const size_t bytes = kCounterBytes + floats * sizeof(float);
   if (slot.second < bytes) {
-    hipError_t e = hipStreamSynchronize(stream);
-    if (e == hipSuccess && slot.first) e = hipFree(slot.first);
+    // Under stream capture (e.g. a HIP graph being recorded) the stream may
+    // not be synchronised and memory it may still use must not be freed: the
+    // old buffer is retired instead, the allocation runs in relaxed capture
+    // mode, and the counter-zeroing kernel becomes part of the graph.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(stream, &cs);
+    const bool capturing = e == hipSuccess && cs != hipStreamCaptureStatusNone;
+    if (e == hipSuccess && slot.first) {
+      if (capturing) {
+        retired().push_back(slot.first);
+      } else {
+        e = hipStreamSynchronize(stream);
+        if (e == hipSuccess) e = hipFree(slot.first);
+      }
+    }
     slot = {nullptr, 0};
     void* p = nullptr;
-    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-    if (e == hipSuccess) e = hipMalloc(&p, want);
+    const size_t want = bytes < (size_t(4) << 20) ? (size_t(4) << 20) : bytes;
+    if (e == hipSuccess) {
+      hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+      if (capturing) (void)hipThreadExchangeStreamCaptureMode(&mode);
+      e = hipMalloc(&p, want);
+      if (capturing) (void)hipThreadExchangeStreamCaptureMode(&mode);
+    }
+    if (e == hipSuccess) e = kh::launch_fill_u32(p, kCounterBytes / 4, 0u, stream);
     if (e != hipSuccess) {
       *rc = hip_fail(op, e);
-      return nullptr;
+      return false;
     }
     slot = {p, want};
   }
   *rc = KH_OK;
-  return static_cast<float*>(slot.first);
+  ws->counters = static_cast<unsigned*>(slot.first);
+  ws->data = reinterpret_cast<float*>(static_cast<char*>(slot.first) + kCounterBytes);
+  return true;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -265,16 +304,17 @@ int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
   }
   kh::QmvArgs a{x->data, x->dtype, w->data, scales->data, biases->data, scales->dtype, res->data,
                 res->dtype, (int)M, (int)N, (int)K, gs, bits, st};
-  const bool fast = transpose && x->dtype != KH_FLOAT32 && aligned16(x->data) && aligned16(w->data);
+  const bool fast = transpose && x->dtype != KH_FLOAT32 && scales->dtype != KH_FLOAT32 &&
+                    aligned16(x->data) && aligned16(w->data);
   hipError_t e;
   if (!fast) {
     e = kh::launch_qmm_generic(a, transpose);
   } else if (M <= 64) {
     e = kh::launch_qmv(a);
   } else {
-    float* ws = workspace(st, (size_t)M * (size_t)(K / gs), &rc, op);
-    if (!ws) return rc;
-    e = kh::launch_qmm(a, ws);
+    Workspace ws;
+    if (!workspace(st, (size_t)M * (size_t)(K / gs), &ws, &rc, op)) return rc;
+    e = kh::launch_qmm(a, ws.data);
   }
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
 }

@@ -206,3 +206,35 @@ def test_errors_raise_kiln_error():
         ops.quantized_matmul(dev(x, "bf16"), dev(L["w"]), dev(L["scales"], "f16"),
                              dev(L["biases"], "f16"), True, 64, 3)
     assert e.value.status == 1 and "bits=3" in str(e.value)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1024, 4096), (3, 272, 1024), (130, 200, 512)])
+def test_graph_capture_replays_match_eager(M, N, K):
+    """The library's launches (split-K counters, workspace) are capturable in a
+    HIP graph; every replay, with eager work in between, equals the eager call."""
+    print(f"case graph M={M} N={N} K={K}", flush=True)
+    L, x = _case(M, N, K, 64, 4, seed=13)
+    xd, w, s, b = dev(x, "bf16"), dev(L["w"]), dev(L["scales"], "f16"), dev(L["biases"], "f16")
+    eager = ops.quantized_matmul(xd, w, s, b, True, 64, 4, out_dtype="f32").clone()
+    out = torch.empty_like(eager)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.quantized_matmul(xd, w, s, b, True, 64, 4, out=out)
+    for r in range(4):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), r
+        ops.quantized_matmul(xd, w, s, b, True, 64, 4, out_dtype="f32")  # eager work between
+        torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("bits,gs,K", [(4, 32, 224), (4, 64, 192), (8, 32, 96), (8, 64, 320), (4, 32, 32)])
+@pytest.mark.parametrize("M", [1, 5, 16, 40])
+def test_qmm_partial_blocks(oracle, bits, gs, K, M):
+    """K that is a multiple of the group size but not of the 16-byte lane block."""
+    print(f"case partial bits={bits} gs={gs} K={K} M={M}", flush=True)
+    N = 48
+    L, x = _case(M, N, K, gs, bits, seed=K + M)
+    y = _run(L, x, gs, bits, "bf16", "f16", "f32")
+    _check_f32(oracle, L, x, gs, bits, "bf16", "f16", y)
