@@ -21,7 +21,11 @@ struct QmvArgs {
   hipStream_t stream;
 };
 
-// Decode path (M <= 64), MFMA on unscaled codes with per-group fp32 scaling.
+// Largest M served by the decode kernel; larger M takes the prefill GEMM.
+constexpr int kDecodeMaxM = 16;
+
+// Decode path (M <= kDecodeMaxM; correct up to M = 64), MFMA on unscaled
+// codes with per-group fp32 scaling.
 hipError_t launch_qmv(const QmvArgs& a);
 
 // Set n 32-bit words to value (a kernel, so it is safe inside graph capture).

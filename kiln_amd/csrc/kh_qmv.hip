@@ -8,19 +8,19 @@
 // weight is ever rounded:
 //   y[m, n] = sum_g  s[n,g] * P'[m,n,g] + (b[n,g] - OFF*s[n,g]) * X[m,g]
 //   P'[m,n,g] = sum_{k in g} x[m,k] * (OFF + q[n,k])      (MFMA, fp32 accumulate)
-//   X[m,g]    = sum_{k in g} x[m,k]                        (fp32, computed once per workgroup)
+//   X[m,g]    = sum_{k in g} x[m,k]                        (MFMA against ones, fp32 accumulate)
 // OFF + q is exactly representable in the MFMA input type: it is built by
 // OR-ing the code into the mantissa of OFF (bf16: OFF = 128, 7-bit mantissa;
 // f16: OFF = 1024, 10-bit mantissa), except 8-bit codes with bf16 activations,
 // which go through an exact int->float conversion with OFF = 0.
 //
-// Work decomposition. One workgroup owns one 16-row output tile (the MFMA
-// column dimension) and all M <= 64 activation rows. Its W waves split the
-// row's code blocks into W contiguous ranges. A block is 16 bytes per lane:
-// the four lane groups of a wave read 4 consecutive words each, 64 contiguous
-// bytes per output row per load instruction (128 codes at 4 bits, 64 at 8).
-// MFMA step j of a block takes word j (4-bit) or words 2j, 2j+1 (8-bit) from
-// every lane group.
+// Work decomposition. One workgroup owns RT 16-row output tiles (MFMA column
+// tiles; RT = 4, 2 or 1, as many as still leave enough workgroups) and all
+// M <= 64 activation rows; its RT*KS waves are (row tile, K slice) pairs, so
+// the staged activations are shared by RT row tiles. A block is 16 bytes per lane: the four lane groups of a wave read 4
+// consecutive words each, 64 contiguous bytes per output row per load
+// instruction (128 codes at 4 bits, 64 at 8). MFMA step j of a block takes
+// word j (4-bit) or words 2j, 2j+1 (8-bit) from every lane group.
 //
 // When a block spans NC > 1 quantization groups (4-bit gs32/gs64, 8-bit
 // gs32), lane groups of different groups must not share an accumulator. Each
@@ -32,13 +32,13 @@
 // inputs whatever the tiling, so results do not depend on M.
 //
 // Per workgroup the activations of the current windows are staged in LDS,
-// permuted into the MFMA pair order, with the per-group sums X and the
-// scales/biases of the tile's rows (converted to fp32, bias pre-offset). The
-// first chunk of code loads is issued before staging so both overlap. Final
-// sums: for every output, chains in ascending order, and within a chain the
-// W wave partials in wave order. W depends only on (N, K, group_size, bits),
-// so every output's summation order is independent of M: row r of the result
-// is bitwise identical for every M <= 64.
+// permuted into the MFMA pair order, with the raw scale/bias halves of the
+// workgroup's rows. The first chunk of code loads is issued
+// before staging so both overlap. Final sums: for every output, chains in
+// ascending order, and within a chain the KS slice partials in slice order.
+// KS depends only on (N, K, group_size, bits), so every output's summation
+// order is independent of M: row r of the result is bitwise identical for
+// every M <= 64.
 //
 // MFMA v_mfma_f32_16x16x32_{bf16,f16}: A = activations (16 rows x 32 k),
 // B = codes (32 k x 16 n). Lane l supplies row/column l%16 and the eight k of
@@ -137,18 +137,25 @@ __device__ __forceinline__ T ldw(const T* p) {
 #endif
 }
 
+#ifndef KH_QMV_ABL
+#define KH_QMV_ABL 0  // tuning ablations: 1 = no staging loads, 2 = no MFMA/epilogue, 3 = no X MFMA
+#endif
 #ifndef KH_QMV_INFLIGHT
-#define KH_QMV_INFLIGHT 32  // VGPRs per lane for one chunk of code loads
+#define KH_QMV_INFLIGHT 16  // VGPRs per lane for one chunk of code loads
 #endif
 #ifndef KH_QMV_WAVE_TARGET
-#define KH_QMV_WAVE_TARGET 8192  // waves per launch to aim for
+#define KH_QMV_WAVE_TARGET 4096  // waves per launch to aim for
 #endif
 #ifndef KH_QMV_MAX_WAVES
-#define KH_QMV_MAX_WAVES 8
+#define KH_QMV_MAX_WAVES 8  // waves per workgroup (row tiles x K slices)
+#endif
+#ifndef KH_QMV_MIN_WGS
+#define KH_QMV_MIN_WGS 256  // workgroups wanted before packing more row tiles per workgroup
 #endif
 #ifndef KH_QMV_LDS
-#define KH_QMV_LDS 49152  // LDS bytes per workgroup for staged activations
+#define KH_QMV_LDS 49152  // LDS bytes per workgroup for staged operands
 #endif
+
 
 constexpr int pow2_floor(int v) {
   int p = 1;
@@ -167,16 +174,16 @@ struct QmvGeom {
   static constexpr int NC = CB >= GS ? CB / GS : 1;   // groups (chains) per block
   static constexpr int BPG = GS > CB ? GS / CB : 1;   // blocks per group
   static constexpr int LGC = 4 / NC;            // lane groups per chain
-  static constexpr int U = KH_QMV_INFLIGHT / 4; // blocks per load chunk
+  static constexpr int U = KH_QMV_INFLIGHT / 8; // blocks per load chunk (two chunks in flight)
 };
 
 struct QmvPlan {
-  int waves;   // K-split waves per workgroup
+  int rt;      // 16-row output tiles per workgroup
+  int ks;      // K slices per workgroup (waves = rt * ks)
   int nct;     // chains per row tile
-  int mt;      // activation rows per chain in a tile (16 / nct)
-  int tiles;   // row tiles
-  int wu;      // units (BPG blocks) per wave staged per round
-  int batch;   // waves staged together (divides waves)
+  int tiles;   // MFMA row tiles
+  int wu;      // units (BPG blocks) per slice staged per round (power of two)
+  int batch;   // slices staged together (power of two, divides ks)
   size_t lds;  // dynamic LDS bytes
 };
 
@@ -185,36 +192,38 @@ static int ceil_div(int a, int b) { return (a + b - 1) / b; }
 template <int BITS, int GS>
 static QmvPlan plan_qmv_t(int M, int N, int K) {
   using Gm = QmvGeom<BITS, GS>;
-  const int NB = ceil_div(K, Gm::CB);
-  const int NU = NB / Gm::BPG;
+  const int NU = ceil_div(K, Gm::CB) / Gm::BPG;  // units per row
   const int tiles16 = ceil_div(N, 16);
-  int waves = 1;
-  while (waves < KH_QMV_MAX_WAVES && tiles16 * waves * 2 <= KH_QMV_WAVE_TARGET && NU / (waves * 2) >= 2)
-    waves *= 2;
+  int rt = 4;
+  while (rt > 1 && tiles16 / rt < KH_QMV_MIN_WGS) rt /= 2;
+  int ks = 1;
+  while (rt * ks * 2 <= KH_QMV_MAX_WAVES && ceil_div(tiles16, rt) * rt * ks * 2 <= KH_QMV_WAVE_TARGET &&
+         NU / (ks * 2) >= 2)
+    ks *= 2;
+  const int rows = 16 * rt;
   int nct = 1;
   if (M <= 16) nct = pow2_floor(16 / M) < Gm::NC ? pow2_floor(16 / M) : Gm::NC;
   const int mt = 16 / nct;
   int mtiles = 1;  // m tiles, rounded up to a power of two (extra tiles see only rows >= M)
   while (mtiles < ceil_div(M, mt)) mtiles *= 2;
   const int tiles = (Gm::NC / nct) * mtiles;
-  // LDS per staged unit: activations, group sums (D-row layout), scale/bias pairs.
-  const size_t per_unit = (size_t)Gm::BPG * Gm::CB * M * 2 + (size_t)tiles * 16 * 4 + 16 * Gm::NC * 8;
-  int batch = waves;
+  // LDS per staged unit: activations and raw scale/bias halves.
+  const size_t per_unit = (size_t)Gm::BPG * Gm::CB * M * 2 + (size_t)rows * Gm::NC * 4;
+  int batch = ks;
   while (batch > 1 && per_unit * batch > KH_QMV_LDS) batch /= 2;
-  int wu = (int)(KH_QMV_LDS / (per_unit * batch));
-  if (wu < 1) wu = 1;
-  if (wu > ceil_div(NU, waves)) wu = ceil_div(NU, waves);
+  int wu = pow2_floor((int)(KH_QMV_LDS / (per_unit * batch)) > 0 ? (int)(KH_QMV_LDS / (per_unit * batch)) : 1);
+  while (wu > 1 && wu / 2 >= ceil_div(NU, ks)) wu /= 2;
   size_t lds = (size_t)batch * wu * per_unit + (size_t)Gm::SPB * M * 16;
-  const size_t red = (size_t)waves * 64 * 16 + (size_t)M * 16 * 4;
+  const size_t red = (size_t)rt * ks * 64 * 16 + (size_t)M * rows * 4;
   if (red > lds) lds = red;
-  return {waves, nct, mt, tiles, wu, batch, lds};
+  return {rt, ks, nct, tiles, wu, batch, lds};
 }
 
 template <int BITS, int GS, bool XBF16, bool SBF16, int TILES>
 __global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    void* __restrict__ out, int odt, int M, int N, int K, int nct, int wu, int batch) {
+    void* __restrict__ out, int odt, int M, int N, int K, int RT, int nct, int wu, int batch) {
   using Gm = QmvGeom<BITS, GS>;
   constexpr int CB = Gm::CB, SPB = Gm::SPB, WPS = Gm::WPS, KBB = Gm::KBB;
   constexpr int NC = Gm::NC, BPG = Gm::BPG, LGC = Gm::LGC, U = Gm::U;
@@ -224,55 +233,60 @@ __global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
 
   const int tid = threadIdx.x;
   const int nthreads = blockDim.x;
-  const int W = nthreads >> 6;
-  const int lw2 = __builtin_ctz(W);
+  const int lrt = __builtin_ctz(RT);
+  const int KS = (nthreads >> 6) >> lrt;        // K slices
+  const int lks = __builtin_ctz(KS);
+  const int ROWS = RT * 16;                     // output rows of this workgroup
+  const int lrows = lrt + 4;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rt = wave & (RT - 1);               // row tile of this wave
+  const int ks = wave >> lrt;                   // K slice of this wave
   const int col = lane & 15;
   const int lg = lane >> 4;
-  const int n = blockIdx.x * 16 + col;
-  const bool nvalid = n < N;
-  const int nc = nvalid ? n : N - 1;  // clamped: every weight load is in bounds
+  const int row0 = blockIdx.x * ROWS;
+  const int n = row0 + rt * 16 + col;
+  const int nc = n < N ? n : N - 1;             // clamped: every weight load is in bounds
   const int G = K / GS;
-  const int WR = K / Gm::CPW;                    // words per row
-  const int NB = (K + CB - 1) / CB;              // blocks per row (last may be partial)
-  const int NU = NB / BPG;                       // units per row
-  const int mt = 16 / nct;                       // rows per chain in a tile
-  const int cgroups = NC / nct;                  // chain groups (tiles per m range)
+  const int WR = K / Gm::CPW;                   // words per row
+  const int NU = ((K + CB - 1) / CB) / BPG;     // units (BPG blocks) per row
+  const int mt = 16 / nct;                      // rows per chain in a tile
+  const int cgroups = NC / nct;                 // chain groups
+  const int lwu = __builtin_ctz(wu), lbatch = __builtin_ctz(batch);
 
-  // LDS carve-up for one staging step: [batch][wu] units of
-  //   xs  : BPG*KBB*M u32x4  permuted activations,
-  //   xd  : TILES*16 floats   group sums in D-row layout,
-  //   sb  : 16*NC float2      (scale, bias - OFF*scale) per tile row and chain,
-  // followed by the zero area (SPB*M u32x4).
-  const int xs_u = BPG * KBB * M;                // u32x4 per unit
+  // LDS for one staging step, `batch` slices x `wu` units, slot = sb_i*wu + ul:
+  //   xs  [slot][BPG*KBB][M] u32x4   permuted activations
+  //   sbh [slot][ROWS][NC]   uint32  scale | bias << 16 (raw halves)
+  // then the zero area [SPB][M] u32x4.
+  const int xs_u = BPG * KBB * M;
+  const int nslots = batch * wu;
   u32x4* xs = reinterpret_cast<u32x4*>(smem);
-  float* xd = reinterpret_cast<float*>(xs + (size_t)batch * wu * xs_u);
-  float2* sb = reinterpret_cast<float2*>(xd + (size_t)batch * wu * TILES * 16);
-  u32x4* zero = reinterpret_cast<u32x4*>(sb + (size_t)batch * wu * 16 * NC);
+  uint32_t* sbh = reinterpret_cast<uint32_t*>(xs + (size_t)nslots * xs_u);
+  u32x4* zero = reinterpret_cast<u32x4*>(sbh + (size_t)nslots * ROWS * NC);
 
-  // Units of each wave: [(NU*v) >> lw2, (NU*(v+1)) >> lw2).
-  const int r0 = (NU * wave) >> lw2;
-  const int r1 = (NU * (wave + 1)) >> lw2;
-  const int longest = (NU + W - 1) >> lw2;
+  // Units of slice k: [(NU*k) >> lks, (NU*(k+1)) >> lks).
+  const int r0 = (NU * ks) >> lks;
+  const int r1 = (NU * (ks + 1)) >> lks;
+  const int longest = (NU + KS - 1) >> lks;
 
-  // Lane roles per tile: row r = col of the A operand; the lane's D rows are
-  // 4*lg .. 4*lg+3, all of one chain because mt is a multiple of 4.
-  int a_off[TILES];   // u32x4 offset of this lane's A operand inside a block (-1: zero lane)
-  int d_chain[TILES]; // chain of this lane's D rows
+  // Lane roles per tile: A row = col; the lane's D rows 4*lg..4*lg+3 belong
+  // to one chain because mt is a multiple of 4.
+  int a_off[TILES];    // u32x4 offset of this lane's A operand inside a block (-1: zero lane)
+  int d_chain[TILES];  // chain of this lane's D rows
 #pragma unroll
   for (int t = 0; t < TILES; ++t) {
     const int cg = t % cgroups, mtile = t / cgroups;
-    const int ca = cg * nct + col / mt, ma = mtile * mt + col % mt;  // chain and row of A row `col`
+    const int ca = cg * nct + col / mt, ma = mtile * mt + col % mt;
     const bool live = (lg / LGC) == ca && ma < M;
-    // k-block of lane group lg, step j, inside a block: lg*SPB + j
-    a_off[t] = live ? (lg * SPB) * M + ma : -1;
+    a_off[t] = live ? (lg * SPB) * M + ma : -1;  // k-block lg*SPB + j, step j
     d_chain[t] = cg * nct + (4 * lg) / mt;
   }
 
   const uint32_t* wrow = w + (int64_t)nc * WR;
   uint32_t mag = XBF16 ? 0x43004300u : 0x64006400u;
   asm volatile("" : "+v"(mag));  // keep it in a VGPR (see codes_to_b)
+  const uint32_t one = XBF16 ? 0x3f803f80u : 0x3c003c00u;  // 1.0 in both halves
+  const u32x4 ones = u32x4{one, one, one, one};
 
   f32x4 acc[TILES];
 #pragma unroll
@@ -280,16 +294,18 @@ __global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
 
   for (int i = tid; i < SPB * M; i += nthreads) zero[i] = u32x4{0u, 0u, 0u, 0u};
 
-  const int nbatch = W / batch;
-  for (int step = 0; step < ((longest + wu - 1) / wu) * nbatch; ++step) {
-    const int off = (step / nbatch) * wu;      // unit offset within every wave's range
-    const int b0 = (step % nbatch) * batch;    // first wave staged in this step
-    const bool mine = wave >= b0 && wave < b0 + batch;
+  const int nbatch = KS >> lbatch;
+  const int nsteps = ((longest + wu - 1) >> lwu) * nbatch;
+  for (int step = 0; step < nsteps; ++step) {
+    const int off = (step / nbatch) << lwu;    // unit offset within every slice
+    const int kb0 = (step % nbatch) << lbatch; // first slice staged in this step
+    const bool mine = ks >= kb0 && ks < kb0 + batch;
     const int my_units = mine ? min(wu, r1 - (r0 + off)) : 0;
     const int my_blocks = my_units * BPG;
-    // ---- first chunk of code loads, issued before staging
-    uint32_t q[U][4];
-    auto load_chunk = [&](int c0) {
+
+    // ---- first two chunks of code loads, issued before staging
+    uint32_t qa[U][4], qb[U][4];
+    auto load_chunk = [&](uint32_t (&q)[U][4], int c0) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int blk = (r0 + off) * BPG + min(c0 + u, max(my_blocks - 1, 0));
@@ -303,79 +319,53 @@ __global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
         q[u][3] = v[3];
       }
     };
-    if (my_blocks > 0) load_chunk(0);
+    if (my_blocks > 0) load_chunk(qa, 0);
+    if (my_blocks > U) load_chunk(qb, U);
 
-    // ---- stage activations, group sums, scales for the batch's units
+    // ---- stage activations and scale/bias halves for the batch's units
     __syncthreads();
     {
-      const int items = batch * wu * BPG * KBB * M;
+      constexpr int LKB = __builtin_ctz(BPG * KBB);
+      const int items = (nslots << LKB);        // (slot, kb); rows m looped inside
       for (int it = tid; it < items; it += nthreads) {
-        const int m = it % M;
-        const int kb = (it / M) % (BPG * KBB);
-        const int ul = (it / (M * BPG * KBB)) % wu;
-        const int vb = it / (M * BPG * KBB * wu);
-        const int v = b0 + vb;
-        const int unit = ((NU * v) >> lw2) + off + ul;
-        const int vend = (NU * (v + 1)) >> lw2;
+        const int kb = it & (BPG * KBB - 1);
+        const int slot = it >> LKB;
+        const int ul = slot & (wu - 1), sb_i = slot >> lwu;
+        const int k_sl = kb0 + sb_i;
+        const int unit = ((NU * k_sl) >> lks) + off + ul;
+        const int uend = (NU * (k_sl + 1)) >> lks;
         const int k = (unit * BPG * KBB + kb) * 8;
-        u32x4 val = u32x4{0u, 0u, 0u, 0u};
-        if (unit < vend && k < K)
-          val = permute_x<BITS>(*reinterpret_cast<const u32x4*>(x + (int64_t)m * K + k));
-        xs[(size_t)(vb * wu + ul) * xs_u + kb * M + m] = val;
+        const bool ok = KH_QMV_ABL != 1 && unit < uend && k < K;
+        u32x4* dst = xs + (size_t)slot * xs_u + kb * M;
+        for (int m = 0; m < M; ++m)
+          dst[m] = ok ? permute_x<BITS>(*reinterpret_cast<const u32x4*>(x + (int64_t)m * K + k))
+                      : u32x4{0u, 0u, 0u, 0u};
       }
-      const int sitems = batch * wu * 16 * NC;
+      constexpr int LNC = __builtin_ctz(NC);
+      const int sitems = (nslots * ROWS) << LNC;  // (slot, row, chain)
       for (int it = tid; it < sitems; it += nthreads) {
-        const int c = it % NC;
-        const int row = (it / NC) % 16;
-        const int ul = (it / (NC * 16)) % wu;
-        const int vb = it / (NC * 16 * wu);
-        const int v = b0 + vb;
-        const int unit = ((NU * v) >> lw2) + off + ul;
-        const int vend = (NU * (v + 1)) >> lw2;
+        const int c = it & (NC - 1);
+        const int ul = (it >> LNC) & (wu - 1);
+        const int row = (it >> (LNC + lwu)) & (ROWS - 1);
+        const int sb_i = it >> (LNC + lwu + lrows);
+        const int k_sl = kb0 + sb_i;
+        const int unit = ((NU * k_sl) >> lks) + off + ul;
+        const int uend = (NU * (k_sl + 1)) >> lks;
         const int g = unit * NC + c;
-        const int rn = min(blockIdx.x * 16 + row, N - 1);
-        float2 e = float2{0.f, 0.f};
-        if (unit < vend && g < G) {
-          const float sc = half_to_f32<SBF16>(scales[(int64_t)rn * G + g]);
-          e = float2{sc, fmaf(-OFF, sc, half_to_f32<SBF16>(biases[(int64_t)rn * G + g]))};
-        }
-        sb[(size_t)(vb * wu + ul) * 16 * NC + row * NC + c] = e;
-      }
-    }
-    __syncthreads();
-    {
-      // group sums in D-row layout: xd[(v*wu+ul)*TILES*16 + t*16 + r]
-      const int items = batch * wu * TILES * 16;
-      for (int it = tid; it < items; it += nthreads) {
-        const int r = it % 16;
-        const int t = (it / 16) % TILES;
-        const int vu = it / (16 * TILES);  // slot: vb*wu + ul
-        const int cg = t % cgroups, mtile = t / cgroups;
-        const int c = cg * nct + r / mt, m = mtile * mt + r % mt;
-        float sum = 0.f;
-        if (m < M) {
-          const u32x4* base = xs + (size_t)vu * xs_u;
-          for (int e = 0; e < GS / 8; ++e) {
-            const int kb = c * (GS / 8) + e;  // k-block within the unit
-            const u32x4 val = base[kb * M + m];
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-              sum += XBF16 ? bf16_bits_to_f32(val[h] & 0xffffu) : f16_bits_to_f32(val[h] & 0xffffu);
-              sum += XBF16 ? bf16_bits_to_f32(val[h] >> 16) : f16_bits_to_f32(val[h] >> 16);
-            }
-          }
-        }
-        xd[it] = sum;
+        const int rn = min(row0 + row, N - 1);
+        uint32_t e = 0u;
+        if (KH_QMV_ABL != 1 && unit < uend && g < G)
+          e = (uint32_t)scales[(int64_t)rn * G + g] | ((uint32_t)biases[(int64_t)rn * G + g] << 16);
+        sbh[((size_t)((sb_i << lwu) + ul) * ROWS + row) * NC + c] = e;
       }
     }
     __syncthreads();
 
     // ---- stream this wave's code blocks
-    const int slot = (wave - b0) * wu;
+    const int slot0 = (ks - kb0) * wu;
     static_assert(BPG == 1 || TILES <= 4, "chains spanning blocks keep one D per tile");
-    f32x4 D[TILES];  // persists across the BPG blocks of a group
-    for (int c0 = 0; c0 < my_blocks; c0 += U) {
-      if (c0 > 0) load_chunk(c0);
+    f32x4 D[TILES], DX[TILES];  // persist across the BPG blocks of a group
+    auto compute_chunk = [&](uint32_t (&q)[U][4], int c0) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int b = c0 + u;
@@ -384,58 +374,76 @@ __global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
         u32x4 B[SPB];
 #pragma unroll
         for (int j = 0; j < SPB; ++j) B[j] = codes_to_b<BITS, XBF16>(&q[u][j * WPS], mag);
-        const u32x4* xunit = xs + (size_t)(slot + ul) * xs_u + bib * KBB * M;
-        const f32x4* xdu = reinterpret_cast<const f32x4*>(xd + (size_t)(slot + ul) * TILES * 16);
-        const float2* sbu = sb + (size_t)(slot + ul) * 16 * NC;
+        if (KH_QMV_ABL == 2) {
+          acc[0][0] += __uint_as_float(B[0][0] ^ B[SPB - 1][3]);
+          continue;
+        }
+        const int slot = slot0 + ul;
+        const u32x4* xunit = xs + (size_t)slot * xs_u + bib * KBB * M;
+        const uint32_t* sbu = sbh + ((size_t)slot * ROWS + rt * 16 + col) * NC;
 #pragma unroll
         for (int t = 0; t < TILES; ++t) {
-          if (bib == 0) D[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (bib == 0) D[t] = DX[t] = f32x4{0.f, 0.f, 0.f, 0.f};
           const u32x4* ap = a_off[t] >= 0 ? xunit + a_off[t] : zero;
 #pragma unroll
-          for (int j = 0; j < SPB; ++j) D[t] = mfma<XBF16>(ap[j * M], B[j], D[t]);
+          for (int j = 0; j < SPB; ++j) {
+            const u32x4 a = ap[j * M];
+            D[t] = mfma<XBF16>(a, B[j], D[t]);
+            if (KH_QMV_ABL != 3) DX[t] = mfma<XBF16>(a, ones, DX[t]);  // group sums X of the same rows
+          }
           if (bib == BPG - 1) {
-            const float2 e = sbu[col * NC + d_chain[t]];
-            const f32x4 X = xdu[t * 4 + lg];
+            const uint32_t e = sbu[d_chain[t]];
+            const float sc = half_to_f32<SBF16>(e & 0xffffu);
+            const float bp = fmaf(-OFF, sc, half_to_f32<SBF16>(e >> 16));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              acc[t][i] = fmaf(e.x, D[t][i], acc[t][i]);
-              acc[t][i] = fmaf(e.y, X[i], acc[t][i]);
+              acc[t][i] = fmaf(sc, D[t][i], acc[t][i]);
+              acc[t][i] = fmaf(bp, DX[t][i], acc[t][i]);
             }
           }
         }
       }
+    };
+    for (int c0 = 0; c0 < my_blocks; c0 += 2 * U) {
+      compute_chunk(qa, c0);
+      if (c0 + 2 * U < my_blocks) load_chunk(qa, c0 + 2 * U);
+      if (c0 + U < my_blocks) {
+        compute_chunk(qb, c0 + U);
+        if (c0 + 3 * U < my_blocks) load_chunk(qb, c0 + 3 * U);
+      }
     }
   }
 
-  // ---- final sums: for each m-tile, chains ascending, waves in order
+  // ---- final sums per output: chains ascending, K slices in order
   __syncthreads();
-  f32x4* red = reinterpret_cast<f32x4*>(smem);                      // [W][64]
-  float* outacc = reinterpret_cast<float*>(red + (size_t)W * 64);   // [M][16]
-  for (int i = tid; i < M * 16; i += nthreads) outacc[i] = 0.f;
+  f32x4* red = reinterpret_cast<f32x4*>(smem);                       // [waves][64]
+  float* outacc = reinterpret_cast<float*>(red + (size_t)nthreads);  // [M][ROWS]
+  for (int i = tid; i < M * ROWS; i += nthreads) outacc[i] = 0.f;
 #pragma unroll
   for (int t = 0; t < TILES; ++t) {
     __syncthreads();
-    red[wave * 64 + lane] = acc[t];
+    red[tid] = acc[t];
     __syncthreads();
-    for (int it = tid; it < 256; it += nthreads) {
-      const int mtile = t / cgroups;
-      const int r_in = it / 16, nl = it % 16;  // (row within chain block, output column)
+    const int mtile = t / cgroups;
+    for (int it = tid; it < 16 * ROWS; it += nthreads) {
+      const int r_in = it >> lrows, row = it & (ROWS - 1);  // (row within chain block, output row)
       const int m = mtile * mt + r_in;
       if (r_in < mt && m < M) {
-        float s = outacc[m * 16 + nl];
+        const int tr = row >> 4, nl = row & 15;
+        float s = outacc[m * ROWS + row];
         for (int cl = 0; cl < nct; ++cl) {
           const int r = cl * mt + r_in;  // D row
-          const int ln = (r / 4) * 16 + nl, el = r % 4;
-          for (int v = 0; v < W; ++v) s += red[v * 64 + ln][el];
+          const int ln = (r >> 2) * 16 + nl, el = r & 3;
+          for (int k2 = 0; k2 < KS; ++k2) s += red[((k2 << lrt) + tr) * 64 + ln][el];
         }
-        outacc[m * 16 + nl] = s;
+        outacc[m * ROWS + row] = s;
       }
     }
   }
   __syncthreads();
-  for (int i = tid; i < M * 16; i += nthreads) {
-    const int m = i / 16, nl = i % 16;
-    const int nn = blockIdx.x * 16 + nl;
+  for (int i = tid; i < M * ROWS; i += nthreads) {
+    const int m = i >> lrows, row = i & (ROWS - 1);
+    const int nn = row0 + row;
     if (nn < N) store_from_f32(out, odt, (int64_t)m * N + nn, outacc[i]);
   }
 }
@@ -443,11 +451,11 @@ __global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
 template <int BITS, int GS, bool XBF16, bool SBF16>
 static hipError_t launch_tiles(const QmvArgs& a) {
   const QmvPlan p = plan_qmv_t<BITS, GS>(a.M, a.N, a.K);
-  const dim3 grid((a.N + 15) / 16), block(64 * p.waves);
-#define KH_QMV_LAUNCH(TV)                                                                       \
-  hipLaunchKernelGGL((qmv_kernel<BITS, GS, XBF16, SBF16, TV>), grid, block, p.lds, a.stream,   \
-                     (const uint16_t*)a.x, (const uint32_t*)a.w, (const uint16_t*)a.scales,    \
-                     (const uint16_t*)a.biases, a.out, a.odt, a.M, a.N, a.K, p.nct, p.wu, p.batch)
+  const dim3 grid((a.N + 16 * p.rt - 1) / (16 * p.rt)), block(64 * p.rt * p.ks);
+#define KH_QMV_LAUNCH(TV)                                                                      \
+  hipLaunchKernelGGL((qmv_kernel<BITS, GS, XBF16, SBF16, TV>), grid, block, p.lds, a.stream,  \
+                     (const uint16_t*)a.x, (const uint32_t*)a.w, (const uint16_t*)a.scales,   \
+                     (const uint16_t*)a.biases, a.out, a.odt, a.M, a.N, a.K, p.rt, p.nct, p.wu, p.batch)
   switch (p.tiles) {
     case 1: KH_QMV_LAUNCH(1); break;
     case 2: KH_QMV_LAUNCH(2); break;

@@ -309,7 +309,7 @@ int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
   hipError_t e;
   if (!fast) {
     e = kh::launch_qmm_generic(a, transpose);
-  } else if (M <= 64) {
+  } else if (M <= kh::kDecodeMaxM) {
     e = kh::launch_qmv(a);
   } else {
     Workspace ws;

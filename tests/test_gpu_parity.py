@@ -113,15 +113,18 @@ def test_qmm_leading_dims_and_empty(oracle):
 
 
 @pytest.mark.parametrize("bits,gs", [(4, 64), (8, 128), (4, 32)])
-def test_rows_are_m_invariant_on_decode_path(bits, gs):
-    """Row r of the result is bitwise the same for every M <= 64 (the property
-    Kiln's calibration probes, crates/kiln-models/src/nn.rs:301-327)."""
+def test_rows_are_m_invariant(bits, gs):
+    """Row r of the result is bitwise the same for every M served by the same
+    kernel: 1..16 (decode) and 17..N (prefill) — the property Kiln's
+    calibration probes (crates/kiln-models/src/nn.rs:301-327)."""
     N, K = 272, 1024
-    L, x = _case(64, N, K, gs, bits, seed=21)
-    full = _run(L, x, gs, bits, "bf16", "f16", "bf16")
-    for M in (1, 2, 5, 16, 17, 33, 63):
-        part = _run(L, x[:M], gs, bits, "bf16", "f16", "bf16")
-        assert np.array_equal(part, full[:M]), M
+    L, x = _case(200, N, K, gs, bits, seed=21)
+    dec = _run(L, x[:16], gs, bits, "bf16", "f16", "bf16")
+    for M in (1, 2, 5, 15):
+        assert np.array_equal(_run(L, x[:M], gs, bits, "bf16", "f16", "bf16"), dec[:M]), M
+    pre = _run(L, x, gs, bits, "bf16", "f16", "bf16")
+    for M in (17, 33, 64, 129):
+        assert np.array_equal(_run(L, x[:M], gs, bits, "bf16", "f16", "bf16"), pre[:M]), M
 
 
 @pytest.mark.parametrize("path", sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz")))
