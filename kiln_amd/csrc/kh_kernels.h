@@ -31,9 +31,11 @@ hipError_t launch_qmv(const QmvArgs& a);
 // Set n 32-bit words to value (a kernel, so it is safe inside graph capture).
 hipError_t launch_fill_u32(void* p, int64_t n, uint32_t value, hipStream_t stream);
 
-// Prefill path (any M; chosen for M > 64): LDS-tiled MFMA GEMM. `xsum` is a
-// device workspace of at least M * (K / gs) floats.
-hipError_t launch_qmm(const QmvArgs& a, float* xsum);
+// Prefill path (any M; chosen for M > kDecodeMaxM): LDS-tiled float16 MFMA
+// GEMM. `ws` is a 16-byte aligned device workspace of qmm_workspace_bytes(M, K)
+// bytes (float16 activations and per-row scales).
+hipError_t launch_qmm(const QmvArgs& a, void* ws);
+size_t qmm_workspace_bytes(int M, int K);
 
 // Any dtype / alignment / transpose: one thread per output, fp32 fma chain.
 hipError_t launch_qmm_generic(const QmvArgs& a, bool transpose);

@@ -1,18 +1,26 @@
-// kh_qmm.hip — prefill quantized GEMM for gfx950 (chosen for M > 64).
+// kh_qmm.hip — prefill quantized GEMM for gfx950 (M > 16).
 //
-// Same factored arithmetic as the decode path (kh_qmv.hip):
-//   y[m,n] = sum_g s[n,g] * P'[m,n,g] + (b[n,g] - OFF*s[n,g]) * X[m,g]
-// with P' = x . (OFF + q) on bf16/f16 MFMA (fp32 accumulate, one fresh chain
-// per group) and X[m,g] = sum of x over the group, computed once per call
-// by qmm_xsum_kernel into a workspace.
+// y[m, n] = sum_k x[m, k] * w[n, k], w = s[n, g(k)] * q[n, k] + b[n, g(k)]
+// (quantized_matmul, transpose=true: crates/kiln-mlx/src/ops.rs:359-388).
 //
-// Tiling: a 256-thread workgroup owns a 128 (m) x 128 (n) output tile and
-// walks K in stages of 64. Per stage it stages the activation tile in LDS as
-// bf16/f16 (already permuted into the pair order of the B operand) and the
-// packed code tile in LDS as raw words (0.5 or 1 byte per weight); each of
-// the four waves (2 x 2, 64 x 64 each) expands its own code fragments in
-// registers right before the MFMA. Global loads of stage s+1 are in flight
-// while stage s computes.
+// Numerics. Each weight is dequantised once, in registers, to float16 with a
+// single rounding: w16 = fma16(s, q, b) (v_pk_fma_f16; q is exact, produced
+// as (1024 + q) - 1024 from the code OR-ed into the mantissa of 1024.0). The
+// activations enter as float16 too: qmm_prep_x converts each row of x to
+// float16 after an exact power-of-two scaling 2^-e_m chosen so that the row's
+// largest magnitude stays below 2^15, and the result row is multiplied back
+// by 2^e_m. Products accumulate in float32 (v_mfma_f32_16x16x32_f16). The
+// only rounding beyond the float32 reference is that of w to float16
+// (relative 2^-11): about 1e-4 relative error on typical outputs, an order
+// of magnitude inside the 1e-3 mean tolerance (rounding w to bfloat16 instead
+// would give ~1.7e-3). Float32 outputs of the same row do not depend on M.
+//
+// Tiling. A 256-thread workgroup owns a 256 (m) x 128 (n) output tile and
+// walks K in stages of 64. Per stage it copies the (pre-permuted) float16
+// activation tile and the raw code tile into LDS; each of its four waves
+// (2 x 2, 128 x 64 each) expands its own code fragments to float16 in
+// registers right before the MFMAs and accumulates directly into the output
+// tile. Global loads of stage s+1 are in flight while stage s computes.
 #include "kh_common.h"
 #include "kh_kernels.h"
 
@@ -20,6 +28,21 @@ namespace kh {
 
 namespace {
 
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 h2;
+
+constexpr int BM = 256, BN = 128, BK = 64, NT = 256;
+constexpr int KB = BK / 8;  // 8-element k-blocks per stage
+constexpr int WM = 128, WN = 64;  // wave tile
+constexpr int MT = WM / 16, NTL = WN / 16;
+constexpr int BPAD = 4;     // words of padding per k-block row of the code tile
+#ifndef KH_QMM_PF
+#define KH_QMM_PF 2
+#endif
+constexpr int PF = KH_QMM_PF;  // stages of global loads in flight
+
+// Pair order of the B operand built from packed codes; the activations are
+// permuted to match. 4-bit word -> (c0,c4)(c1,c5)(c2,c6)(c3,c7);
+// 8-bit word pair -> (c0,c2)(c1,c3)(c4,c6)(c5,c7).
 template <int BITS>
 __device__ __forceinline__ u32x4 permute_x(u32x4 d) {
   u32x4 r;
@@ -37,94 +60,99 @@ __device__ __forceinline__ u32x4 permute_x(u32x4 d) {
   return r;
 }
 
-template <int BITS, bool XBF16>
-__device__ __forceinline__ u32x4 codes_to_b(uint32_t q0, uint32_t q1) {
-  u32x4 r;
-  constexpr uint32_t MAG = XBF16 ? 0x43004300u : 0x64006400u;
+// Pairs of codes as float16 (1024 + q) in both halves (exact for q < 1024).
+template <int BITS>
+__device__ __forceinline__ void code_pairs(uint32_t q0, uint32_t q1, uint32_t mag, uint32_t* r) {
   if constexpr (BITS == 4) {
-    r[0] = (q0 & 0x000f000fu) | MAG;
-    r[1] = ((q0 >> 4) & 0x000f000fu) | MAG;
-    r[2] = ((q0 >> 8) & 0x000f000fu) | MAG;
-    r[3] = ((q0 >> 12) & 0x000f000fu) | MAG;
-  } else if constexpr (!XBF16) {
-    r[0] = (q0 & 0x00ff00ffu) | MAG;
-    r[1] = ((q0 >> 8) & 0x00ff00ffu) | MAG;
-    r[2] = (q1 & 0x00ff00ffu) | MAG;
-    r[3] = ((q1 >> 8) & 0x00ff00ffu) | MAG;
+    r[0] = (q0 & 0x000f000fu) | mag;
+    r[1] = ((q0 >> 4) & 0x000f000fu) | mag;
+    r[2] = ((q0 >> 8) & 0x000f000fu) | mag;
+    r[3] = ((q0 >> 12) & 0x000f000fu) | mag;
   } else {
-    const uint32_t qq[2] = {q0, q1};
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t u = qq[h];
-      const uint32_t f0 = __float_as_uint((float)(u & 0xffu));
-      const uint32_t f1 = __float_as_uint((float)((u >> 8) & 0xffu));
-      const uint32_t f2 = __float_as_uint((float)((u >> 16) & 0xffu));
-      const uint32_t f3 = __float_as_uint((float)(u >> 24));
-      r[2 * h + 0] = perm(f2, f0, 0x07060302u);
-      r[2 * h + 1] = perm(f3, f1, 0x07060302u);
-    }
+    r[0] = (q0 & 0x00ff00ffu) | mag;
+    r[1] = ((q0 >> 8) & 0x00ff00ffu) | mag;
+    r[2] = (q1 & 0x00ff00ffu) | mag;
+    r[3] = ((q1 >> 8) & 0x00ff00ffu) | mag;
   }
-  return r;
 }
 
-template <bool XBF16>
-__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
-  if constexpr (XBF16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
-
-constexpr int BM = 128, BN = 128, BK = 64, NT = 256;
-constexpr int KB = BK / 8;     // 8-element k-blocks per stage
-constexpr int BPAD = 16;       // LDS row padding (words) of the code tile
 
 }  // namespace
 
-// xsum[m, g] = sum_{k in group g} x[m, k], float32, increasing k.
-__global__ void qmm_xsum_kernel(const uint16_t* __restrict__ x, int xbf16, float* __restrict__ xsum,
-                                int M, int K, int gs) {
-  const int G = K / gs;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)M * G) return;
-  const int64_t m = i / G, g = i % G;
-  const u32x4* src = reinterpret_cast<const u32x4*>(x + m * K + g * gs);
-  float s = 0.f;
-  for (int c = 0; c < gs / 8; ++c) {
-    const u32x4 v = src[c];
+// xh[m] = permuted float16 of x[m] * 2^-e_m, rscale[m] = 2^e_m, with e_m >= 0
+// the smallest exponent keeping max|x[m]| * 2^-e_m below 2^15. One
+// workgroup per row.
+template <int BITS, bool XBF16>
+__global__ __launch_bounds__(256) void qmm_prep_x(const uint16_t* __restrict__ x,
+                                                  u32x4* __restrict__ xh,
+                                                  float* __restrict__ rscale, int K) {
+  __shared__ float red[256];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const u32x4* row = reinterpret_cast<const u32x4*>(x + (int64_t)m * K);
+  const int nb = K / 8;
+  float mx = 0.f;
+  for (int c = tid; c < nb; c += 256) {
+    const u32x4 v = row[c];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t lo = v[e] & 0xffffu, hi = v[e] >> 16;
-      s += xbf16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-      s += xbf16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+      const float lo = XBF16 ? bf16_bits_to_f32(v[e] & 0xffffu) : f16_bits_to_f32(v[e] & 0xffffu);
+      const float hi = XBF16 ? bf16_bits_to_f32(v[e] >> 16) : f16_bits_to_f32(v[e] >> 16);
+      mx = fmaxf(mx, fmaxf(fabsf(lo), fabsf(hi)));
     }
   }
-  xsum[i] = s;
+  red[tid] = mx;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
+    __syncthreads();
+  }
+  mx = red[0];
+  int ex = 0;
+  if (mx >= 32768.f) {
+    int e2;
+    (void)frexpf(mx, &e2);  // mx = f * 2^e2, f in [0.5, 1)
+    ex = e2 - 15;           // mx * 2^-ex < 2^15
+  }
+  const float inv = ldexpf(1.f, -ex);
+  if (tid == 0) rscale[m] = ldexpf(1.f, ex);
+  u32x4* dst = xh + (int64_t)m * nb;
+  for (int c = tid; c < nb; c += 256) {
+    const u32x4 v = row[c];
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = XBF16 ? bf16_bits_to_f32(v[e] & 0xffffu) : f16_bits_to_f32(v[e] & 0xffffu);
+      const float hi = XBF16 ? bf16_bits_to_f32(v[e] >> 16) : f16_bits_to_f32(v[e] >> 16);
+      o[e] = f32_to_f16_bits(lo * inv) | (f32_to_f16_bits(hi * inv) << 16);
+    }
+    dst[c] = permute_x<BITS>(o);
+  }
 }
 
-template <int BITS, int GS, bool XBF16>
-__global__ __launch_bounds__(NT) void qmm_kernel(const uint16_t* __restrict__ x,
+template <int BITS, int GS, bool SF16>
+__global__ __launch_bounds__(NT) void qmm_kernel(const u32x4* __restrict__ xh,
                                                  const uint32_t* __restrict__ w,
-                                                 const void* __restrict__ scales,
-                                                 const void* __restrict__ biases, int sdt,
-                                                 const float* __restrict__ xsum,
+                                                 const uint16_t* __restrict__ scales,
+                                                 const uint16_t* __restrict__ biases,
+                                                 const float* __restrict__ rscale,
                                                  void* __restrict__ out, int odt, int M, int N,
                                                  int K) {
   constexpr int CPW = 32 / BITS;
   constexpr int WPS = 8 / CPW;                 // words per 8-k block
   constexpr int WPR = BK / CPW;                // words per row per stage
   constexpr int GPS = GS >= BK ? 1 : BK / GS;  // groups touched per stage
-  constexpr float OFF = (BITS == 8 && XBF16) ? 0.0f : (XBF16 ? 128.0f : 1024.0f);
   constexpr int BROW = BN * WPS + BPAD;        // words per k-block row of the code tile
   constexpr int AV = BM * KB / NT;             // 16-byte activation chunks per thread
   constexpr int BV = BN * WPR / 4 / NT;        // 16-byte code chunks per thread
 
   __shared__ u32x4 As[KB * BM];
   __shared__ uint32_t Bs[KB * BROW];
-  __shared__ float2 Sc[GPS * BN];
-  __shared__ float Xs[GPS * BM];
+  __shared__ uint32_t Ss[GPS * BN];  // f16 scales: (s, s); bf16 scales: f32 bits of s
+  __shared__ uint32_t Bb[GPS * BN];  // f16: (b, b);     bf16: f32 bits of b
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -133,55 +161,57 @@ __global__ __launch_bounds__(NT) void qmm_kernel(const uint16_t* __restrict__ x,
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int G = K / GS;
   const int64_t WR = K / CPW;
+  const int KB8 = K / 8;
   const int nst = (K + BK - 1) / BK;
 
-  u32x4 ra[AV], rb[BV];
-  float2 rs = {0.f, 0.f};
-  float rx = 0.f;
+  // Prefetch ring: stage st lives in registers slot st % PF until stored to LDS.
+  u32x4 ra[PF][AV], rb[PF][BV];
+  uint32_t rs[PF], rbb[PF];
 
-  auto load_stage = [&](int st) {
-    const int k0 = st * BK;
+  auto load_stage = [&](int p, int st) {
+    const int kb0 = st * KB;
 #pragma unroll
     for (int r = 0; r < AV; ++r) {
       const int c = tid + r * NT;
       const int mm = c / KB, kb = c % KB;
-      const int m = m0 + mm, k = k0 + kb * 8;
-      ra[r] = (m < M && k < K) ? *reinterpret_cast<const u32x4*>(x + (int64_t)m * K + k)
-                               : u32x4{0u, 0u, 0u, 0u};
+      const int m = m0 + mm;
+      ra[p][r] = (m < M && kb0 + kb < KB8) ? xh[(int64_t)m * KB8 + kb0 + kb] : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int r = 0; r < BV; ++r) {
       const int c = tid + r * NT;
       const int nn = c / (WPR / 4), wq = c % (WPR / 4);
       const int n = n0 + nn;
-      const int64_t word = (int64_t)k0 / CPW + wq * 4;
-      rb[r] = (n < N && word < WR)
-                  ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + n * WR + word))
-                  : u32x4{0u, 0u, 0u, 0u};
+      const int64_t word = (int64_t)st * WPR + wq * 4;
+      rb[p][r] = (n < N && word < WR) ? *reinterpret_cast<const u32x4*>(w + n * WR + word)
+                                      : u32x4{0u, 0u, 0u, 0u};
     }
     if (tid < GPS * BN) {
       const int gi = tid / BN, nn = tid % BN;
-      const int g = k0 / GS + gi, n = n0 + nn;
-      rs = float2{0.f, 0.f};
+      const int g = (st * BK) / GS + gi, n = n0 + nn;
+      rs[p] = rbb[p] = 0u;
       if (n < N && g < G) {
-        const float sc = load_as_f32(scales, sdt, (int64_t)n * G + g);
-        rs = float2{sc, fmaf(-OFF, sc, load_as_f32(biases, sdt, (int64_t)n * G + g))};
+        const uint32_t sh = scales[(int64_t)n * G + g], bh = biases[(int64_t)n * G + g];
+        if constexpr (SF16) {
+          rs[p] = sh | (sh << 16);
+          rbb[p] = bh | (bh << 16);
+        } else {
+          rs[p] = __float_as_uint(bf16_bits_to_f32(sh));
+          rbb[p] = __float_as_uint(bf16_bits_to_f32(bh));
+        }
       }
-    }
-    if (tid >= NT - GPS * BM) {
-      const int t2 = tid - (NT - GPS * BM);
-      const int gi = t2 / BM, mm = t2 % BM;
-      const int g = k0 / GS + gi, m = m0 + mm;
-      rx = (m < M && g < G) ? xsum[(int64_t)m * G + g] : 0.f;
     }
   };
 
-  auto store_stage = [&]() {
+  // Activation tile: k-block kb of row m at As[kb*BM + (m ^ kb)] — the XOR
+  // spreads the eight k-blocks of a row (stored by neighbouring threads) over
+  // different banks; readers of one k-block see a permutation of 16 rows.
+  auto store_stage = [&](int p) {
 #pragma unroll
     for (int r = 0; r < AV; ++r) {
       const int c = tid + r * NT;
       const int mm = c / KB, kb = c % KB;
-      As[kb * BM + mm] = permute_x<BITS>(ra[r]);
+      As[kb * BM + (mm ^ kb)] = ra[p][r];
     }
 #pragma unroll
     for (int r = 0; r < BV; ++r) {
@@ -190,111 +220,139 @@ __global__ __launch_bounds__(NT) void qmm_kernel(const uint16_t* __restrict__ x,
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int word = wq * 4 + e;  // word within the stage row
-        const int kb = word / WPS, sub = word % WPS;
-        Bs[kb * BROW + nn * WPS + sub] = rb[r][e];
+        Bs[(word / WPS) * BROW + nn * WPS + word % WPS] = rb[p][r][e];
       }
     }
-    if (tid < GPS * BN) Sc[tid] = rs;
-    if (tid >= NT - GPS * BM) Xs[tid - (NT - GPS * BM)] = rx;
+    if (tid < GPS * BN) {
+      Ss[tid] = rs[p];
+      Bb[tid] = rbb[p];
+    }
   };
 
-  f32x4 acc[4][4], P[4][4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) acc[t][u] = P[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint32_t mag = 0x64006400u;  // float16 1024.0 in both halves
+  asm volatile("" : "+v"(mag));  // a VGPR operand, so (mask, or) fuses into v_and_or_b32
 
-  load_stage(0);
-  for (int st = 0; st < nst; ++st) {
+  f32x4 acc[MT][NTL];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int u = 0; u < NTL; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int p = 0; p < PF; ++p)
+    if (p < nst) load_stage(p, p);
+  for (int st0 = 0; st0 < nst; st0 += PF) {
+#pragma unroll
+  for (int p = 0; p < PF; ++p) {
+    const int st = st0 + p;
+    if (st >= nst) continue;  // uniform
     __syncthreads();
-    store_stage();
+    store_stage(p);
     __syncthreads();
-    if (st + 1 < nst) load_stage(st + 1);
+    if (st + PF < nst) load_stage(p, st + PF);
 
 #pragma unroll
     for (int j = 0; j < BK / 32; ++j) {
-      const int kabs = st * BK + j * 32;
-      if (kabs % GS == 0) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int u = 0; u < 4; ++u) P[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
       const int kb = 4 * j + lg;
-      u32x4 a[4], b[4];
+      const int gi = GS >= BK ? 0 : (j * 32) / GS;
+      u32x4 b[NTL];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) a[t] = As[kb * BM + wm * 64 + t * 16 + col];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int nn = wn * 64 + u * 16 + col;
+      for (int u = 0; u < NTL; ++u) {
+        const int nn = wn * WN + u * 16 + col;
         const uint32_t q0 = Bs[kb * BROW + nn * WPS];
         const uint32_t q1 = WPS == 2 ? Bs[kb * BROW + nn * WPS + 1] : 0u;
-        b[u] = codes_to_b<BITS, XBF16>(q0, q1);
-      }
+        uint32_t r[4];
+        code_pairs<BITS>(q0, q1, mag, r);
+        if constexpr (SF16) {
+          const h2 s2 = __builtin_bit_cast(h2, Ss[gi * BN + nn]);
+          const h2 b2 = __builtin_bit_cast(h2, Bb[gi * BN + nn]);
+          const h2 k1024 = h2{(_Float16)1024.f, (_Float16)1024.f};
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+          for (int i = 0; i < 4; ++i)
+            b[u][i] = __builtin_bit_cast(
+                uint32_t, __builtin_elementwise_fma(s2, __builtin_bit_cast(h2, r[i]) - k1024, b2));
+        } else {
+          const float sf = __uint_as_float(Ss[gi * BN + nn]);
+          const float bf = __uint_as_float(Bb[gi * BN + nn]);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) P[t][u] = mfma<XBF16>(a[t], b[u], P[t][u]);
-
-      if ((kabs + 32) % GS == 0) {
-        const int gi = GS >= BK ? 0 : (j * 32) / GS;
-        float2 sb[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) sb[u] = Sc[gi * BN + wn * 64 + u * 16 + col];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const f32x4 xs = *reinterpret_cast<const f32x4*>(&Xs[gi * BM + wm * 64 + t * 16 + 4 * lg]);
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              acc[t][u][i] = fmaf(sb[u].x, P[t][u][i], acc[t][u][i]);
-              acc[t][u][i] = fmaf(sb[u].y, xs[i], acc[t][u][i]);
-            }
+          for (int i = 0; i < 4; ++i) {
+            // (1024 + q) - 1024 is exact; one rounding in the fma, one to f16
+            const float lo = fmaf(sf, f16_bits_to_f32(r[i] & 0xffffu) - 1024.f, bf);
+            const float hi = fmaf(sf, f16_bits_to_f32(r[i] >> 16) - 1024.f, bf);
+            b[u][i] = f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+          }
         }
       }
-    }
-  }
-
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < MT; ++t) {
+        const u32x4 a = As[kb * BM + ((wm * WM + t * 16 + col) ^ kb)];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int n = n0 + wn * 64 + u * 16 + col;
-      if (n >= N) continue;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = m0 + wm * 64 + t * 16 + 4 * lg + i;
-        if (m < M) store_from_f32(out, odt, (int64_t)m * N + n, acc[t][u][i]);
+        for (int u = 0; u < NTL; ++u) acc[t][u] = mfma_f16(a, b[u], acc[t][u]);
       }
     }
+  }
+  }
+
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + wm * WM + t * 16 + 4 * lg + i;
+      if (m >= M) continue;
+      const float rsc = rscale[m];
+#pragma unroll
+      for (int u = 0; u < NTL; ++u) {
+        const int n = n0 + wn * WN + u * 16 + col;
+        if (n < N) store_from_f32(out, odt, (int64_t)m * N + n, acc[t][u][i] * rsc);
+      }
+    }
+  }
 }
 
-template <int BITS, bool XBF16>
-static hipError_t launch_gs(const QmvArgs& a, float* xsum) {
+size_t qmm_workspace_bytes(int M, int K) {
+  return (size_t)M * K * 2 + (size_t)M * sizeof(float) + 256;
+}
+
+template <int BITS, int GS>
+static hipError_t launch_sf(const QmvArgs& a, const u32x4* xh, const float* rsc) {
   const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM), block(NT);
-#define KH_QMM_LAUNCH(GSV)                                                                      \
-  hipLaunchKernelGGL((qmm_kernel<BITS, GSV, XBF16>), grid, block, 0, a.stream,                  \
-                     (const uint16_t*)a.x, (const uint32_t*)a.w, a.scales, a.biases, a.sdt, xsum, \
-                     a.out, a.odt, a.M, a.N, a.K)
-  switch (a.gs) {
-    case 32: KH_QMM_LAUNCH(32); break;
-    case 64: KH_QMM_LAUNCH(64); break;
-    default: KH_QMM_LAUNCH(128); break;
-  }
-#undef KH_QMM_LAUNCH
+  if (a.sdt == DT_F16)
+    hipLaunchKernelGGL((qmm_kernel<BITS, GS, true>), grid, block, 0, a.stream, xh,
+                       (const uint32_t*)a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases,
+                       rsc, a.out, a.odt, a.M, a.N, a.K);
+  else
+    hipLaunchKernelGGL((qmm_kernel<BITS, GS, false>), grid, block, 0, a.stream, xh,
+                       (const uint32_t*)a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases,
+                       rsc, a.out, a.odt, a.M, a.N, a.K);
   return hipGetLastError();
 }
 
-hipError_t launch_qmm(const QmvArgs& a, float* xsum) {
-  const int64_t total = (int64_t)a.M * (a.K / a.gs);
-  hipLaunchKernelGGL(qmm_xsum_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, a.stream,
-                     (const uint16_t*)a.x, a.xdt == DT_BF16 ? 1 : 0, xsum, a.M, a.K, a.gs);
+template <int BITS>
+static hipError_t launch_gs(const QmvArgs& a, const u32x4* xh, const float* rsc) {
+  switch (a.gs) {
+    case 32: return launch_sf<BITS, 32>(a, xh, rsc);
+    case 64: return launch_sf<BITS, 64>(a, xh, rsc);
+    default: return launch_sf<BITS, 128>(a, xh, rsc);
+  }
+}
+
+// `ws` holds qmm_workspace_bytes(M, K) bytes (16-byte aligned). Scales and
+// biases are float16 or bfloat16.
+hipError_t launch_qmm(const QmvArgs& a, void* ws) {
+  u32x4* xh = static_cast<u32x4*>(ws);
+  float* rsc = reinterpret_cast<float*>(static_cast<char*>(ws) + (size_t)a.M * a.K * 2);
+  const bool xbf16 = a.xdt == DT_BF16;
+#define KH_PREP(B, X) \
+  hipLaunchKernelGGL((qmm_prep_x<B, X>), dim3(a.M), dim3(256), 0, a.stream, (const uint16_t*)a.x, xh, rsc, a.K)
+  if (a.bits == 4) {
+    if (xbf16) KH_PREP(4, true); else KH_PREP(4, false);
+  } else {
+    if (xbf16) KH_PREP(8, true); else KH_PREP(8, false);
+  }
+#undef KH_PREP
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const bool xbf16 = a.xdt == DT_BF16;
-  if (a.bits == 4) return xbf16 ? launch_gs<4, true>(a, xsum) : launch_gs<4, false>(a, xsum);
-  return xbf16 ? launch_gs<8, true>(a, xsum) : launch_gs<8, false>(a, xsum);
+  return a.bits == 4 ? launch_gs<4>(a, xh, rsc) : launch_gs<8>(a, xh, rsc);
 }
 
 }  // namespace kh

@@ -313,7 +313,8 @@ int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
     e = kh::launch_qmv(a);
   } else {
     Workspace ws;
-    if (!workspace(st, (size_t)M * (size_t)(K / gs), &ws, &rc, op)) return rc;
+    const size_t bytes = kh::qmm_workspace_bytes((int)M, (int)K);
+    if (!workspace(st, (bytes + 3) / 4, &ws, &rc, op)) return rc;
     e = kh::launch_qmm(a, ws.data);
   }
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
