@@ -1,7 +1,7 @@
 /*
  * kiln_hip.h — C ABI of the MI355X (gfx950) affine-quantized linear path.
  *
- * Drop-in for the four mlx-c entry points Kiln's quantized layers reach:
+ * Drop-in for the mlx-c entry points Kiln's quantized layers reach:
  *
  *   kh_quantized_matmul     replaces mlx_quantized_matmul, bound at
  *                           crates/kiln-mlx/src/ops.rs:374-385 and wrapped by
@@ -12,6 +12,9 @@
  *                           (ops::dequantize, ops.rs:456-484).
  *   kh_take                 replaces mlx_take_axis for axis 0, bound at
  *                           ops.rs:250-254 (ops::take).
+ *   kh_add                  replaces mlx_add for the bias add of Linear::forward
+ *                           (nn.rs:98-100, ops::add): res = a + b, b broadcast
+ *                           over a's leading dimensions.
  *   kh_quantized_embedding  the fused form of Embedding::lookup
  *                           (nn.rs:159-176): three take(axis=0) calls
  *                           followed by dequantize, in one pass.
@@ -103,6 +106,11 @@ typedef enum kh_status {
  * x: bfloat16 | float16 | float32; scales/biases: bfloat16 | float16 | float32
  * (same dtype for both); res: bfloat16 | float16 | float32. Products are
  * accumulated in float32 and rounded once (round-to-nearest-even) to res.
+ * With bf16/f16 x and bf16/f16 scales, transpose=true and M <= 16 every
+ * dequantised weight is used exactly; for M > 16 each weight is rounded once
+ * to float16 (relative error <= 2^-11) before the float32-accumulating MFMA,
+ * and x is scaled per row by an exact power of two into float16 range. Other
+ * combinations run an exact float32 kernel.
  * bits in {4, 8}; group_size in {32, 64, 128}; K % group_size == 0. */
 int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
                         const kh_array* scales, const kh_array* biases,
@@ -134,6 +142,11 @@ int kh_quantized_embedding(kh_array* res, const kh_array* ids,
                            const kh_array* biases, kh_optional_int group_size,
                            kh_optional_int bits, const char* mode,
                            kh_stream stream);
+
+/* res = a + b, elementwise, with b broadcast over a's leading dimensions
+ * (b.shape == a.shape[a.ndim - b.ndim:]). a, b, res: bfloat16|float16|float32;
+ * res has a's shape. Each sum is formed in float32 and rounded once to res. */
+int kh_add(kh_array* res, const kh_array* a, const kh_array* b, kh_stream stream);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* kh_last_error(void);

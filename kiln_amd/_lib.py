@@ -22,7 +22,7 @@ STATUS = {0: "KH_OK", 1: "KH_ERR_INVALID_ARGUMENT", 2: "KH_ERR_UNSUPPORTED",
 
 # Every symbol include/kiln_hip.h declares.
 EXPORTS = ("kh_quantized_matmul", "kh_dequantize", "kh_take", "kh_quantized_embedding",
-           "kh_last_error", "kh_version")
+           "kh_add", "kh_last_error", "kh_version")
 
 
 class KhArray(ctypes.Structure):
@@ -58,9 +58,11 @@ def lib() -> ctypes.CDLL:
         L.kh_dequantize.argtypes = [P, P, P, P, KhOptionalInt, KhOptionalInt, ctypes.c_char_p,
                                     ctypes.c_void_p]
         L.kh_take.argtypes = [P, P, P, ctypes.c_void_p]
+        L.kh_add.argtypes = [P, P, P, ctypes.c_void_p]
         L.kh_quantized_embedding.argtypes = [P, P, P, P, P, KhOptionalInt, KhOptionalInt,
                                              ctypes.c_char_p, ctypes.c_void_p]
-        for f in ("kh_quantized_matmul", "kh_dequantize", "kh_take", "kh_quantized_embedding"):
+        for f in ("kh_quantized_matmul", "kh_dequantize", "kh_take", "kh_quantized_embedding",
+                  "kh_add"):
             getattr(L, f).restype = ctypes.c_int
         L.kh_last_error.restype = ctypes.c_char_p
         L.kh_version.restype = ctypes.c_char_p

@@ -16,6 +16,9 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+HOST = os.path.join(HERE, "host")
+RUNNER_SRC = os.path.join(os.path.dirname(HERE), "tests", "cpp", "kiln_host_run.cpp")
+RUNNER = os.path.join(HERE, "kiln_host_run")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkiln_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -45,7 +48,7 @@ def build(verbose: bool = False, out: str = LIB, extra=(), build_dir: str = BUIL
     """Compile and link; `extra` adds hipcc flags, `out`/`build_dir` redirect
     the library and objects (used to build tuning variants side by side)."""
     os.makedirs(build_dir, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip"))) + sorted(glob.glob(os.path.join(HOST, "*.cpp")))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(lambda s: _compile(s, build_dir, extra), srcs))
     tmp = out + ".tmp"
@@ -56,7 +59,22 @@ def build(verbose: bool = False, out: str = LIB, extra=(), build_dir: str = BUIL
     os.replace(tmp, out)
     if verbose:
         print(f"built {out}")
+    if out == LIB and os.path.exists(RUNNER_SRC):
+        build_runner(verbose)
     return out
+
+
+def build_runner(verbose: bool = False) -> str:
+    """The C++ host-layer test driver, linked against libkiln_hip.so."""
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", RUNNER_SRC, "-o", RUNNER + ".tmp", f"-L{HERE}", "-lkiln_hip",
+           "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"building the host test driver failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(RUNNER + ".tmp", RUNNER)
+    if verbose:
+        print(f"built {RUNNER}")
+    return RUNNER
 
 
 if __name__ == "__main__":

@@ -150,6 +150,13 @@ __global__ void qmm_generic_kernel(const void* __restrict__ x, int xdt,
   }
 }
 
+__global__ void add_kernel(const void* __restrict__ a, int adt, const void* __restrict__ b, int bdt,
+                           void* __restrict__ res, int rdt, int64_t n, int64_t nb) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  store_from_f32(res, rdt, i, load_as_f32(a, adt, i) + load_as_f32(b, bdt, i % nb));
+}
+
 __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -158,6 +165,14 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v)
 inline unsigned blocks_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
 }  // namespace
+
+hipError_t launch_add(const void* a, int adt, const void* b, int bdt, void* res, int rdt, int64_t n,
+                      int64_t nb, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, a, adt, b, bdt, res,
+                     rdt, n, nb);
+  return hipGetLastError();
+}
 
 hipError_t launch_fill_u32(void* p, int64_t n, uint32_t value, hipStream_t stream) {
   if (n == 0) return hipSuccess;

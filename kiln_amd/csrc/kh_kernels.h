@@ -50,6 +50,10 @@ hipError_t launch_embedding(const void* ids, bool ids_signed, int64_t T, const v
                             const void* scales, const void* biases, int sdt, void* out, int odt,
                             int64_t V, int64_t H, int gs, int bits, hipStream_t stream);
 
+// res[i] = a[i] + b[i % nb] (float32 sum, rounded once to rdt).
+hipError_t launch_add(const void* a, int adt, const void* b, int bdt, void* res, int rdt, int64_t n,
+                      int64_t nb, hipStream_t stream);
+
 // take(a, ids, axis=0) on rows of row_bytes bytes.
 hipError_t launch_take(const void* a, int64_t V, int64_t row_bytes, const void* ids,
                        bool ids_signed, int64_t T, void* out, hipStream_t stream);

@@ -374,6 +374,31 @@ int kh_take(kh_array* res, const kh_array* a, const kh_array* indices, kh_stream
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
 }
 
+int kh_add(kh_array* res, const kh_array* a, const kh_array* b, kh_stream stream) {
+  const char* op = "add";
+  int rc;
+  if ((rc = check_array(a, op, "a")) || (rc = check_array(b, op, "b"))) return rc;
+  if (!is_float(a->dtype) || !is_float(b->dtype))
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] operands must be float16/bfloat16/float32, got %s and %s",
+                op, dtype_name(a->dtype), dtype_name(b->dtype));
+  if (b->ndim > a->ndim)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] cannot broadcast %s onto %s", op, shape_str(b).c_str(),
+                shape_str(a).c_str());
+  for (int i = 0; i < b->ndim; ++i)
+    if (b->shape[i] != a->shape[a->ndim - b->ndim + i])
+      return fail(KH_ERR_INVALID_ARGUMENT, "[%s] cannot broadcast %s onto %s", op, shape_str(b).c_str(),
+                  shape_str(a).c_str());
+  kh_array want = *a;
+  if ((rc = check_result(op, res, want))) return rc;
+  const int64_t n = numel(a), nb = numel(b);
+  if (n == 0) return KH_OK;
+  if (nb == 0) return fail(KH_ERR_INVALID_ARGUMENT, "[%s] empty addend for non-empty array", op);
+  if ((rc = check_device(op))) return rc;
+  hipError_t e = kh::launch_add(a->data, a->dtype, b->data, b->dtype, res->data, res->dtype, n, nb,
+                                static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? KH_OK : hip_fail(op, e);
+}
+
 int kh_quantized_embedding(kh_array* res, const kh_array* ids, const kh_array* w,
                            const kh_array* scales, const kh_array* biases,
                            kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,

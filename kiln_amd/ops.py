@@ -137,6 +137,17 @@ def take(a: torch.Tensor, indices: torch.Tensor, axis: int = 0, *,
     return out
 
 
+def add(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None,
+        stream=None) -> torch.Tensor:
+    """a + b with b broadcast over a's leading dims (Linear's bias add,
+    crates/kiln-models/src/nn.rs:98-100)."""
+    if out is None:
+        out = torch.empty_like(a, dtype=result_dtype(a.dtype, b.dtype))
+    _check(_lib.lib().kh_add(_desc(out, "res"), _desc(a, "a"), _desc(b, "b"),
+                             _stream_handle(a, stream)))
+    return out
+
+
 def quantized_embedding(ids: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                         biases: torch.Tensor, group_size: int = 64, bits: int = 4, *,
                         mode: str = "affine", out_dtype=None, out: torch.Tensor | None = None,

@@ -1,0 +1,184 @@
+// kiln_host_run — drives the C++ host layer (kiln_amd/host) for the tests.
+//
+//   kiln_host_run selftest            checks that need no GPU (JSON reader,
+//                                     config validation, error paths)
+//   kiln_host_run job <job.json>      loads a checkpoint directory and runs one
+//                                     layer call on the GPU, writing raw output
+//
+// job.json: {"model_dir": d, "op": "linear"|"embed"|"as_linear"|"probe"|"load",
+//            "prefix": p, "input": file, "input_shape": [...],
+//            "input_dtype": "bfloat16"|"float16"|"float32"|"uint32"|"int32",
+//            "output": file}
+// It prints one JSON line: {"ok": true, "shape": [...], "dtype": ...} or
+// {"ok": false, "error": "..."}; "probe" prints {"ok": true, "m": first
+// divergent M}; "load" prints the linear's io_features and remaining tensors.
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <iostream>
+#include <sstream>
+#include <string>
+
+#include "../../kiln_amd/host/kiln_host.hpp"
+
+using namespace kiln;
+
+static int fails = 0;
+#define CHECK(cond)                                                   \
+  do {                                                                \
+    if (!(cond)) {                                                    \
+      std::fprintf(stderr, "CHECK failed %s:%d: %s\n", __FILE__, __LINE__, #cond); \
+      ++fails;                                                        \
+    }                                                                 \
+  } while (0)
+
+static std::string jstr(const std::string& s) {
+  std::string o = "\"";
+  for (char c : s) {
+    if (c == '"' || c == '\\') o += '\\';
+    if (c == '\n') {
+      o += "\\n";
+      continue;
+    }
+    o += c;
+  }
+  return o + "\"";
+}
+
+static int selftest() {
+  // JSON reader
+  auto v = json::parse(R"({"a": [1, 2.5, -3e2], "b": {"c": "x\"yé"}, "t": true, "n": null})");
+  CHECK(v.is_object());
+  CHECK(v.get("a")->arr.size() == 3 && v.get("a")->arr[2].num == -300.0);
+  CHECK(v.get("b")->get("c")->str == "x\"y\xc3\xa9");
+  CHECK(v.get("t")->b && v.get("n")->kind == json::Value::Null);
+  bool threw = false;
+  try {
+    json::parse("{\"a\": [1, 2}");
+  } catch (const std::exception&) {
+    threw = true;
+  }
+  CHECK(threw);
+
+  // config validation (crates/kiln-models/src/config.rs:137-148, 735-760)
+  CHECK(validate_quant_params(Quantization{64, 4}).ok());
+  CHECK(validate_quant_params(Quantization{128, 8}).ok());
+  auto bad = validate_quant_params(Quantization{64, 3});
+  CHECK(!bad.ok() && bad.error().message.find("bits=3 group_size=64") != std::string::npos);
+  CHECK(!validate_quant_params(Quantization{48, 4}).ok());
+  CHECK(validate_quant_params(std::nullopt).ok());
+  auto mode = validate_quantization(json::parse(R"({"quantization": {"group_size": 64, "bits": 4, "mode": "mxfp4"}})"));
+  CHECK(!mode.ok() && mode.error().message.find("\"mxfp4\"") != std::string::npos);
+  auto over = validate_quantization(json::parse(
+      R"({"quantization": {"group_size": 64, "bits": 4, "model.layers.0.mlp": {"bits": 8}, "a": 1}})"));
+  CHECK(!over.ok() && over.error().message.find("[\"a\", \"model.layers.0.mlp\"]") != std::string::npos);
+  auto q = quantization_from_config(json::parse(R"({"quantization": {"group_size": 32, "bits": 8}})"));
+  CHECK(q.ok() && q.value() && q.value()->group_size == 32 && q.value()->bits == 8);
+  auto none = quantization_from_config(json::parse(R"({"hidden_size": 8})"));
+  CHECK(none.ok() && !none.value());
+  auto domain = quantization_from_config(json::parse(R"({"quantization": {"group_size": 16, "bits": 4}})"));
+  CHECK(!domain.ok());
+
+  // missing checkpoint is an error, not an abort
+  auto store = WeightStore::from_model_dir("/nonexistent-kiln-dir", Stream::gpu());
+  CHECK(!store.ok() && store.error().message.find("failed to read") != std::string::npos);
+
+  // dtype sizes
+  CHECK(dtype_size(Dtype::Bfloat16) == 2 && dtype_size(Dtype::Uint32) == 4);
+
+  std::printf("{\"ok\": %s, \"failures\": %d}\n", fails ? "false" : "true", fails);
+  return fails ? 1 : 0;
+}
+
+static Dtype parse_dtype(const std::string& s) {
+  if (s == "bfloat16") return Dtype::Bfloat16;
+  if (s == "float16") return Dtype::Float16;
+  if (s == "float32") return Dtype::Float32;
+  if (s == "uint32") return Dtype::Uint32;
+  return Dtype::Int32;
+}
+
+static int fail_json(const std::string& msg) {
+  std::printf("{\"ok\": false, \"error\": %s}\n", jstr(msg).c_str());
+  return 2;
+}
+
+static int job(const std::string& path) {
+  std::ifstream f(path);
+  std::stringstream ss;
+  ss << f.rdbuf();
+  json::Value j = json::parse(ss.str());
+  const std::string dir = j.get("model_dir")->str, op = j.get("op")->str, prefix = j.get("prefix")->str;
+  Stream s = Stream::gpu();
+
+  std::ifstream cf(dir + "/config.json");
+  std::stringstream cs;
+  cs << cf.rdbuf();
+  auto quant = quantization_from_config(json::parse(cs.str()));
+  if (!quant) return fail_json(quant.error().message);
+  auto store = WeightStore::from_model_dir(dir, s);
+  if (!store) return fail_json(store.error().message);
+
+  if (op == "load") {
+    auto l = nn::Linear::load(store.value(), prefix, quant.value());
+    if (!l) return fail_json(l.error().message);
+    auto io = l.value().io_features();
+    std::string rem = "[";
+    for (const auto& n : store.value().remaining()) rem += (rem.size() > 1 ? ", " : "") + jstr(n);
+    std::printf("{\"ok\": true, \"in\": %lld, \"out\": %lld, \"quantized\": %s, \"remaining\": %s]}\n",
+                (long long)io.first, (long long)io.second, l.value().quantized() ? "true" : "false",
+                rem.c_str());
+    return 0;
+  }
+
+  std::vector<int64_t> shape;
+  for (const auto& d : j.get("input_shape")->arr) shape.push_back((int64_t)d.num);
+  std::ifstream inf(j.get("input")->str, std::ios::binary);
+  std::string in((std::istreambuf_iterator<char>(inf)), std::istreambuf_iterator<char>());
+  auto x = Array::from_bytes(in.data(), in.size(), shape, parse_dtype(j.get("input_dtype")->str), s);
+  if (!x) return fail_json(x.error().message);
+
+  Result<Array> y = Error{"unknown op " + op};
+  if (op == "linear") {
+    auto l = nn::Linear::load(store.value(), prefix, quant.value());
+    if (!l) return fail_json(l.error().message);
+    y = l.value().forward(x.value(), s);
+  } else if (op == "embed" || op == "as_linear" || op == "probe") {
+    auto e = nn::Embedding::load(store.value(), prefix, quant.value());
+    if (!e) return fail_json(e.error().message);
+    if (op == "embed") {
+      y = e.value().lookup(x.value(), s);
+    } else if (op == "as_linear") {
+      y = e.value().as_linear(x.value(), s);
+    } else {
+      const nn::Embedding& emb = e.value();
+      auto m = nn::probe_row_stability((int64_t)j.get("k")->num, x.value(), s,
+                                       [&](const Array& xx) { return emb.as_linear(xx, s); });
+      if (!m) return fail_json(m.error().message);
+      std::printf("{\"ok\": true, \"m\": %d}\n", m.value());
+      return 0;
+    }
+  }
+  if (!y) return fail_json(y.error().message);
+  auto bytes = y.value().to_bytes(s);
+  if (!bytes) return fail_json(bytes.error().message);
+  std::ofstream of(j.get("output")->str, std::ios::binary);
+  of.write(reinterpret_cast<const char*>(bytes.value().data()), (std::streamsize)bytes.value().size());
+  std::string sh = "[";
+  for (int i = 0; i < y.value().ndim(); ++i) sh += (i ? ", " : "") + std::to_string(y.value().dim(i));
+  std::printf("{\"ok\": true, \"shape\": %s], \"dtype\": \"%s\"}\n", sh.c_str(), dtype_name(y.value().dtype()));
+  return 0;
+}
+
+int main(int argc, char** argv) {
+  if (argc >= 2 && std::strcmp(argv[1], "selftest") == 0) return selftest();
+  if (argc >= 3 && std::strcmp(argv[1], "job") == 0) {
+    try {
+      return job(argv[2]);
+    } catch (const std::exception& e) {
+      return fail_json(e.what());
+    }
+  }
+  std::fprintf(stderr, "usage: kiln_host_run selftest | job <job.json>\n");
+  return 64;
+}

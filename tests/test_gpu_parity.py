@@ -254,3 +254,30 @@ def test_qmm_partial_blocks(oracle, bits, gs, K, M):
     L, x = _case(M, N, K, gs, bits, seed=K + M)
     y = _run(L, x, gs, bits, "bf16", "f16", "f32")
     _check_f32(oracle, L, x, gs, bits, "bf16", "f16", y)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("adt,bdt,odt", [(torch.bfloat16, torch.bfloat16, torch.bfloat16),
+                                         (torch.float16, torch.float16, torch.float16),
+                                         (torch.bfloat16, torch.float32, torch.float32),
+                                         (torch.float16, torch.bfloat16, torch.float16)])
+@pytest.mark.parametrize("shape,bshape", [((5, 96), (96,)), ((2, 3, 4101), (4101,)),
+                                          ((2, 3, 8), (3, 8)), ((0, 16), (16,))])
+def test_add_broadcast_bit_exact(adt, bdt, odt, shape, bshape):
+    """kh_add: each sum formed in float32 and rounded once (RNE) to the output
+    dtype — the same as IEEE float32 addition followed by one cast."""
+    g = torch.Generator().manual_seed(7)
+    a = torch.randn(shape, generator=g).to(adt).cuda()
+    b = torch.randn(bshape, generator=g).to(bdt).cuda()
+    out = torch.empty(shape, dtype=odt, device="cuda")
+    ops.add(a, b, out=out)
+    ref = (a.float() + b.float()).to(odt)
+    assert torch.equal(out.view(-1).cpu().view(torch.int16 if odt != torch.float32 else torch.int32),
+                       ref.view(-1).cpu().view(torch.int16 if odt != torch.float32 else torch.int32))
+
+
+@pytest.mark.gpu
+def test_add_rejects_non_suffix_broadcast():
+    a = torch.zeros((4, 8), dtype=torch.float16, device="cuda")
+    with pytest.raises(ops.KilnError):
+        ops.add(a, torch.zeros((4,), dtype=torch.float16, device="cuda"))

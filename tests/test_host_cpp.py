@@ -1,0 +1,131 @@
+"""The C++ host layer (kiln_amd/host, driven by tests/cpp/kiln_host_run.cpp):
+safetensors loading (single file and sharded index, weights.rs:45-106),
+config validation (config.rs:137-148, 735-760), Linear (nn.rs:51-114) with
+its bias add, Embedding lookup and tied head (nn.rs:116-194), and the row
+stability probe (nn.rs:301-327) — checked against the CPU oracle."""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from kiln_amd.workloads import make_linear_numpy, make_x_numpy
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+RUNNER = os.path.join(ROOT, "kiln_amd", "kiln_host_run")
+
+
+def _run(*args, timeout=120):
+    r = subprocess.run([RUNNER, *args], capture_output=True, text=True, timeout=timeout)
+    line = r.stdout.strip().splitlines()[-1] if r.stdout.strip() else "{}"
+    return r.returncode, json.loads(line), r.stderr
+
+
+def test_selftest_without_gpu():
+    if not os.path.exists(RUNNER):
+        pytest.skip("host test driver not built")
+    rc, out, err = _run("selftest")
+    assert rc == 0 and out["ok"], err
+
+
+def _checkpoint(tmp_path, sharded):
+    from safetensors.numpy import save_file
+    gs, bits = 64, 4
+    lin = make_linear_numpy(96, 256, gs, "q4", seed=31)
+    emb = make_linear_numpy(200, 256, gs, "emb", seed=32)
+    bias = (np.random.default_rng(33).standard_normal(96) * 0.1).astype(np.float16)
+    tensors = {
+        "model.layers.0.mlp.gate_proj.weight": lin["w"],
+        "model.layers.0.mlp.gate_proj.scales": lin["scales"].view(np.float16),
+        "model.layers.0.mlp.gate_proj.biases": lin["biases"].view(np.float16),
+        "model.layers.0.mlp.gate_proj.bias": bias,
+        "model.embed_tokens.weight": emb["w"],
+        "model.embed_tokens.scales": emb["scales"].view(np.float16),
+        "model.embed_tokens.biases": emb["biases"].view(np.float16),
+        "model.norm.weight": np.ones(256, dtype=np.float16),
+    }
+    d = tmp_path / ("sharded" if sharded else "single")
+    d.mkdir()
+    if sharded:
+        names = sorted(tensors)
+        a, b = names[: len(names) // 2], names[len(names) // 2:]
+        save_file({k: tensors[k] for k in a}, str(d / "model-00001-of-00002.safetensors"))
+        save_file({k: tensors[k] for k in b}, str(d / "model-00002-of-00002.safetensors"))
+        wm = {k: "model-00001-of-00002.safetensors" for k in a}
+        wm.update({k: "model-00002-of-00002.safetensors" for k in b})
+        (d / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": wm}))
+    else:
+        save_file(tensors, str(d / "model.safetensors"))
+    (d / "config.json").write_text(json.dumps({"model_type": "llama",
+                                               "quantization": {"group_size": gs, "bits": bits}}))
+    return d, lin, emb, bias
+
+
+def _job(tmp_path, **kw):
+    p = tmp_path / f"job_{kw['op']}.json"
+    p.write_text(json.dumps(kw))
+    return _run("job", str(p))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("sharded", [False, True])
+def test_linear_embedding_head_from_checkpoint(oracle, tmp_path, sharded):
+    d, lin, emb, bias = _checkpoint(tmp_path, sharded)
+    rc, out, err = _job(tmp_path, model_dir=str(d), op="load", prefix="model.layers.0.mlp.gate_proj")
+    assert rc == 0 and out["ok"], (out, err)
+    assert (out["in"], out["out"], out["quantized"]) == (256, 96, True)
+    assert "model.norm.weight" in out["remaining"] and "model.embed_tokens.weight" in out["remaining"]
+
+    # Linear::forward = quantized_matmul(transpose=true) + bias (f16 x -> f16 y)
+    x = make_x_numpy(5, 256, seed=34, xdt="f16")
+    (tmp_path / "x.bin").write_bytes(x.tobytes())
+    rc, out, err = _job(tmp_path, model_dir=str(d), op="linear", prefix="model.layers.0.mlp.gate_proj",
+                        input=str(tmp_path / "x.bin"), input_shape=[5, 256], input_dtype="float16",
+                        output=str(tmp_path / "y.bin"))
+    assert rc == 0 and out["ok"], (out, err)
+    assert out["shape"] == [5, 96] and out["dtype"] == "float16"
+    y = np.frombuffer((tmp_path / "y.bin").read_bytes(), dtype=np.float16).astype(np.float64).reshape(5, 96)
+    ref16 = oracle.quantized_matmul(x, "f16", lin["w"], lin["scales"], lin["biases"], "f16", 64, 4, True, "f16")
+    ref = (oracle.to_f32(ref16, "f16") + bias.astype(np.float32)).astype(np.float16).astype(np.float64)
+    assert np.max(np.abs(y - ref)) <= 2e-2 * np.max(np.abs(ref))
+    assert np.mean(np.abs(y - ref)) <= 1e-3 * np.mean(np.abs(ref))
+
+    # Embedding::lookup, bit-exact (gather + dequantize)
+    ids = np.array([[0, 199, 7], [7, 3, 100]], dtype=np.uint32)
+    (tmp_path / "ids.bin").write_bytes(ids.tobytes())
+    rc, out, err = _job(tmp_path, model_dir=str(d), op="embed", prefix="model.embed_tokens",
+                        input=str(tmp_path / "ids.bin"), input_shape=[2, 3], input_dtype="uint32",
+                        output=str(tmp_path / "e.bin"))
+    assert rc == 0 and out["ok"] and out["shape"] == [2, 3, 256], (out, err)
+    e = np.frombuffer((tmp_path / "e.bin").read_bytes(), dtype=np.uint16).reshape(2, 3, 256)
+    assert np.array_equal(e, oracle.embedding(ids, emb["w"], emb["scales"], emb["biases"], "f16", 64, 4, "f16"))
+
+    # Embedding::as_linear (tied head), f16 hidden -> f16 logits
+    h = make_x_numpy(3, 256, seed=35, xdt="f16")
+    (tmp_path / "h.bin").write_bytes(h.tobytes())
+    rc, out, err = _job(tmp_path, model_dir=str(d), op="as_linear", prefix="model.embed_tokens",
+                        input=str(tmp_path / "h.bin"), input_shape=[1, 3, 256], input_dtype="float16",
+                        output=str(tmp_path / "l.bin"))
+    assert rc == 0 and out["ok"] and out["shape"] == [1, 3, 200], (out, err)
+    lg = np.frombuffer((tmp_path / "l.bin").read_bytes(), dtype=np.float16).astype(np.float64).reshape(3, 200)
+    lref = oracle.to_f32(oracle.quantized_matmul(h, "f16", emb["w"], emb["scales"], emb["biases"], "f16",
+                                                 64, 4, True, "f16"), "f16").astype(np.float64)
+    assert np.mean(np.abs(lg - lref)) <= 1e-3 * np.mean(np.abs(lref))
+
+    # probe_row_stability: rows are bit-stable for every M the decode kernel serves
+    base = make_x_numpy(1, 64, seed=36, xdt="f16")
+    (tmp_path / "b.bin").write_bytes(base.tobytes())
+    rc, out, err = _job(tmp_path, model_dir=str(d), op="probe", prefix="model.embed_tokens", k=256,
+                        input=str(tmp_path / "b.bin"), input_shape=[1, 1, 64], input_dtype="float16")
+    assert rc == 0 and out["ok"], (out, err)
+    assert out["m"] >= 17
+
+
+@pytest.mark.gpu
+def test_missing_quantization_block_is_an_error(tmp_path):
+    d, *_ = _checkpoint(tmp_path, False)
+    (d / "config.json").write_text(json.dumps({"model_type": "llama"}))
+    rc, out, err = _job(tmp_path, model_dir=str(d), op="load", prefix="model.layers.0.mlp.gate_proj")
+    assert rc == 2 and not out["ok"]
+    assert "no quantization block" in out["error"]
