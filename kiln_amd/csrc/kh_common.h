@@ -66,4 +66,24 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// Pair order in which the decode kernels turn packed codes into 16-bit
+// operand pairs; activations are permuted to match. 4-bit word -> (c0,c4)(c1,c5)(c2,c6)(c3,c7);
+// 8-bit word pair -> (c0,c2)(c1,c3)(c4,c6)(c5,c7).
+template <int BITS>
+__device__ __forceinline__ u32x4 permute_x(u32x4 d) {
+  u32x4 r;
+  if constexpr (BITS == 4) {
+    r[0] = perm(d[2], d[0], 0x05040100u);
+    r[1] = perm(d[2], d[0], 0x07060302u);
+    r[2] = perm(d[3], d[1], 0x05040100u);
+    r[3] = perm(d[3], d[1], 0x07060302u);
+  } else {
+    r[0] = perm(d[1], d[0], 0x05040100u);
+    r[1] = perm(d[1], d[0], 0x07060302u);
+    r[2] = perm(d[3], d[2], 0x05040100u);
+    r[3] = perm(d[3], d[2], 0x07060302u);
+  }
+  return r;
+}
+
 }  // namespace kh

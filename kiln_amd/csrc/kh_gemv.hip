@@ -1,0 +1,371 @@
+// kh_gemv.hip — decode quantized GEMV for gfx950 at M <= 4: one pass over
+// the packed weights, every load issued up front, VALU dot products.
+//
+// Computes y[m, n] = sum_k x[m, k] * (s[n, g(k)] * q[n, k] + b[n, g(k)])
+// (the transpose=true form of quantized_matmul, crates/kiln-mlx/src/ops.rs:359-388,
+// called by Linear::forward nn.rs:89 and Embedding::as_linear nn.rs:187).
+//
+// Layout. A row of packed codes is a sequence of 16-byte chunks (32 codes at
+// 4 bits, 16 at 8 bits); a chunk never straddles a quantization group since
+// group_size >= 32. Lane slot t of a workgroup (W waves, 64*W slots) owns
+// chunks c = t + i*64*W, i < I, of every one of the workgroup's R rows, so
+// one load instruction of a wave reads 1 KB of contiguous weight bytes, and
+// the lane's activations for its chunks are loaded once and kept in
+// registers for all R rows.
+//
+// Arithmetic. Per chunk, the codes become 16-bit pairs OFF + q (bf16
+// OFF = 128, f16 OFF = 1024, built by OR-ing the code into the mantissa;
+// 8-bit codes with bf16 activations convert exactly through float32 with
+// OFF = 0) and meet the activations, permuted into the same pair order, in a
+// v_dot2c_f32_{bf16,f16} chain. Every product is exact; the affine terms
+// are applied per chunk as
+//   acc += s * P + (b - OFF*s) * X,   P = sum x*(OFF+q),  X = sum x
+// so no dequantised weight is ever rounded.
+//
+// Reduction, in a fixed order: chunks i ascending within a lane; across the
+// 64 lanes of a wave a butterfly over lane offsets 32, 16, ..., 1 whose
+// first steps also split the R*M partial sums among lanes; across waves in
+// wave order through LDS. Each output's summation tree is the same whatever
+// M is, so row r of the result is bitwise identical for every M this kernel
+// serves.
+#include "kh_common.h"
+#include "kh_kernels.h"
+
+namespace kh {
+
+#ifndef KH_GEMV_WAVES
+#define KH_GEMV_WAVES 2048  // waves per launch wanted before fewer rows per workgroup
+#endif
+
+#ifndef KH_GEMV_RMAX
+#define KH_GEMV_RMAX 16  // rows per workgroup with one chunk per lane slot
+#endif
+#ifndef KH_GEMV_ABL
+#define KH_GEMV_ABL 0  // tuning ablations: 1 = no arithmetic on codes, 2 = no scale/bias loads
+#endif
+#ifndef KH_GEMV_NT
+#define KH_GEMV_NT 1  // weight loads marked non-temporal (streamed once)
+#endif
+
+namespace {
+
+constexpr int kGemvMaxWaves = 8;
+
+// Raw buffer loads: a descriptor per tensor (uniform, in SGPRs), the row
+// offset as the scalar offset and a 32-bit lane offset, so no per-lane 64-bit
+// address arithmetic. Tensors are below 4 GiB (checked by the host). The
+// third descriptor word 0x00020000 is the gfx9-family raw buffer format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7fffffff, 0x00020000);
+}
+
+constexpr int kCodeAux = KH_GEMV_NT ? 2 : 0;  // nt: weights are streamed once
+
+template <int BITS, bool XBF16>
+struct GemvOff {
+  static constexpr float value = (BITS == 8 && XBF16) ? 0.0f : (XBF16 ? 128.0f : 1024.0f);
+};
+
+template <bool XBF16>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  if constexpr (XBF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a), __builtin_bit_cast(bf2, b), c,
+                                           false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+}
+
+// One 16-byte chunk of codes -> NP operand pairs in permute_x order:
+// 4-bit word j gives pairs 4j+t = (c_t, c_{t+4}) of that word; 8-bit word j
+// gives pairs 2j = (c0, c2), 2j+1 = (c1, c3). `mag` holds OFF in both halves
+// in a VGPR, so each (mask, or) is one v_and_or_b32.
+template <int BITS, bool XBF16>
+__device__ __forceinline__ void chunk_pairs(const uint32_t (&q)[4], uint32_t mag,
+                                            uint32_t (&p)[64 / BITS]) {
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = q[j];
+      p[4 * j + 0] = (u & 0x000f000fu) | mag;
+      p[4 * j + 1] = ((u >> 4) & 0x000f000fu) | mag;
+      p[4 * j + 2] = ((u >> 8) & 0x000f000fu) | mag;
+      p[4 * j + 3] = ((u >> 12) & 0x000f000fu) | mag;
+    }
+  } else if constexpr (!XBF16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      p[2 * j + 0] = (q[j] & 0x00ff00ffu) | mag;
+      p[2 * j + 1] = ((q[j] >> 8) & 0x00ff00ffu) | mag;
+    }
+  } else {
+    // Codes 0..255 are exact in bf16: the upper half of the float32 bits.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = q[j];
+      const uint32_t f0 = __float_as_uint((float)(u & 0xffu));
+      const uint32_t f1 = __float_as_uint((float)((u >> 8) & 0xffu));
+      const uint32_t f2 = __float_as_uint((float)((u >> 16) & 0xffu));
+      const uint32_t f3 = __float_as_uint((float)(u >> 24));
+      p[2 * j + 0] = perm(f2, f0, 0x07060302u);
+      p[2 * j + 1] = perm(f3, f1, 0x07060302u);
+    }
+  }
+}
+
+template <bool SBF16>
+__device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
+  return SBF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+
+// Wave butterfly at lane offset O, then O/2, ..., 1. While more than one
+// partial remains (CNT > 1), a step halves the set each lane carries: the
+// lane with bit O clear keeps the lower half, its partner the upper half, and
+// each adds the partner's copy of the half it keeps; after log2(NV) steps
+// lane l carries partial l >> (6 - log2(NV)). Later steps sum that survivor.
+// Float addition is commutative, so both lanes of a pair form the same sum
+// and every output sees the same tree over the 64 lanes whatever NV is.
+template <int CNT, int O>
+__device__ __forceinline__ void butterfly(float* acc, int lane) {
+  if constexpr (O >= 1) {
+    if constexpr (CNT > 1) {
+      constexpr int H = CNT / 2;
+      const bool up = (lane & O) != 0;
+#pragma unroll
+      for (int j = 0; j < H; ++j) {
+        const float send = up ? acc[j] : acc[j + H];
+        const float keep = up ? acc[j + H] : acc[j];
+        acc[j] = keep + __shfl_xor(send, O);
+      }
+      butterfly<H, O / 2>(acc, lane);
+    } else {
+      acc[0] += __shfl_xor(acc[0], O);
+      butterfly<1, O / 2>(acc, lane);
+    }
+  }
+}
+
+template <int BITS, bool XBF16, bool SBF16, int M, int R, int I>
+__global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    void* __restrict__ out, int odt, int Mrows, int N, int K, int cshift) {
+  constexpr int CPC = 128 / BITS;  // codes per chunk
+  constexpr int NP = CPC / 2;      // operand pairs per chunk
+  constexpr int NXV = CPC / 8;     // 16-byte activation loads per chunk
+  constexpr int NV = R * M;        // partial sums per lane
+  constexpr float OFF = GemvOff<BITS, XBF16>::value;
+  static_assert(NV <= 64 && (NV & (NV - 1)) == 0, "partials must split evenly over lanes");
+
+  __shared__ float red[kGemvMaxWaves][NV];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int nth = blockDim.x;
+  const int nch = K / CPC;           // chunks per row
+  const int wpr = nch * 4;           // words per row
+  const int G = nch >> cshift;       // groups per row (cshift = log2(group_size / CPC))
+  const int row0 = blockIdx.x * R;
+
+  int cidx[I];
+  bool live[I];
+#pragma unroll
+  for (int i = 0; i < I; ++i) {
+    const int c = tid + i * nth;
+    live[i] = c < nch;
+    cidx[i] = live[i] ? c : nch - 1;  // clamped: every load stays in bounds
+  }
+
+  // ---- issue every load: activations, codes, scale/bias halves. Each
+  // address is a row base (uniform across the wave) plus a 32-bit lane
+  // offset, the form the scalar-base global loads take.
+  const __amdgpu_buffer_rsrc_t bx = buffer_of(x), bw = buffer_of(w);
+  const __amdgpu_buffer_rsrc_t bs = buffer_of(scales), bb = buffer_of(biases);
+  u32x4 xr[I][M][NXV];
+#pragma unroll
+  for (int i = 0; i < I; ++i)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const int mm = m < Mrows ? m : Mrows - 1;
+#pragma unroll
+      for (int v = 0; v < NXV; ++v)
+        xr[i][m][v] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(bx, cidx[i] * (CPC * 2) + v * 16, mm * K * 2, 0));
+    }
+  // Row by row (codes, then that row's scale and bias halves), so that row r
+  // can be computed as soon as its own loads have landed.
+  uint32_t q[R][I][4];
+  uint32_t sr[R][I], br[R][I];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = row0 + r < N ? row0 + r : N - 1;
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+      const u32x4 v = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(bw, cidx[i] * 16, n * wpr * 4, kCodeAux));
+      q[r][i][0] = v[0];
+      q[r][i][1] = v[1];
+      q[r][i][2] = v[2];
+      q[r][i][3] = v[3];
+      const int go = (cidx[i] >> cshift) * 2;
+      if (KH_GEMV_ABL == 2) {
+        sr[r][i] = 0x3c00u + r;
+        br[r][i] = 0x3c00u + go;
+      } else {
+        sr[r][i] = __builtin_amdgcn_raw_buffer_load_b16(bs, go, n * G * 2, 0);
+        br[r][i] = __builtin_amdgcn_raw_buffer_load_b16(bb, go, n * G * 2, 0);
+      }
+    }
+  }
+
+  // Nothing below may be scheduled above this point: every load of the wave
+  // is in flight before the first one is waited for (one memory round trip).
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- activations into pair order; X = sum of the chunk's activations
+  uint32_t xw[I][M][NP];
+  float X[I][M];
+  const uint32_t one = XBF16 ? 0x3f803f80u : 0x3c003c00u;
+#pragma unroll
+  for (int i = 0; i < I; ++i)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      // Lanes past the row end and rows m >= Mrows hold clamped (finite,
+      // in-bounds) data: their sums are discarded, not masked here.
+#pragma unroll
+      for (int v = 0; v < NXV; ++v) {
+        const u32x4 pv = permute_x<BITS>(xr[i][m][v]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xw[i][m][4 * v + e] = pv[e];
+      }
+      float s = 0.f;
+#pragma unroll
+      for (int k = 0; k < NP; ++k) s = dot2<XBF16>(xw[i][m][k], one, s);
+      X[i][m] = s;
+    }
+
+  uint32_t mag = XBF16 ? 0x43004300u : 0x64006400u;
+  asm volatile("" : "+v"(mag));  // keep it in a VGPR (see chunk_pairs)
+
+  float acc[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) acc[j] = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+      if (KH_GEMV_ABL == 1) {
+        acc[r * M] += __uint_as_float((q[r][i][0] ^ q[r][i][1] ^ q[r][i][2] ^ q[r][i][3] ^ sr[r][i] ^ br[r][i]) & 0x3fffffffu);
+        continue;
+      }
+      uint32_t p[NP];
+      chunk_pairs<BITS, XBF16>(q[r][i], mag, p);
+      const float sc = half_bits_to_f32<SBF16>(sr[r][i]);
+      const float bp = fmaf(-OFF, sc, half_bits_to_f32<SBF16>(br[r][i]));
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float d = 0.f;
+#pragma unroll
+        for (int k = 0; k < NP; ++k) d = dot2<XBF16>(p[k], xw[i][m][k], d);
+        // a select, not a branch: a branch would let the compiler sink this
+        // row's loads into it, behind the waits for the other rows
+        const float a = fmaf(bp, X[i][m], fmaf(sc, d, acc[r * M + m]));
+        acc[r * M + m] = live[i] ? a : acc[r * M + m];
+      }
+    }
+
+  // ---- wave butterfly over lane offsets 32..1
+  butterfly<NV, 32>(acc, lane);
+  constexpr int LNV = __builtin_ctz(NV);
+  if ((lane & ((64 >> LNV) - 1)) == 0) red[wave][lane >> (6 - LNV)] = acc[0];
+  __syncthreads();
+  if (tid < NV) {
+    const int W = nth >> 6;
+    float s = red[0][tid];
+    for (int v = 1; v < W; ++v) s += red[v][tid];
+    const int r = tid / M, m = tid % M;
+    const int n = row0 + r;
+    if (n < N && m < Mrows) store_from_f32(out, odt, (int64_t)m * N + n, s);
+  }
+}
+
+struct GemvPlan {
+  int waves, I, R;
+};
+
+GemvPlan plan_gemv(int N, int K, int bits) {
+  const int nch = K * bits / 128;
+  int I = 1;
+  while ((nch + 64 * I - 1) / (64 * I) > kGemvMaxWaves) ++I;
+  const int waves = (nch + 64 * I - 1) / (64 * I);
+  int R = I == 1 ? KH_GEMV_RMAX : (I == 2 ? 4 : 2);
+  while (R > 2 && (int64_t)((N + R - 1) / R) * waves < KH_GEMV_WAVES) R >>= 1;
+  return {waves, I, R};
+}
+
+template <int BITS, bool XBF16, bool SBF16, int M, int R, int I>
+hipError_t launch_one(const QmvArgs& a, const GemvPlan& p) {
+  constexpr int CPC = 128 / BITS;
+  const int cshift = __builtin_ctz(a.gs / CPC);
+  hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, R, I>), dim3((a.N + R - 1) / R),
+                     dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, (const uint32_t*)a.w,
+                     (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.out, a.odt, a.M, a.N,
+                     a.K, cshift);
+  return hipGetLastError();
+}
+
+template <int BITS, bool XBF16, bool SBF16, int M>
+hipError_t launch_m(const QmvArgs& a, const GemvPlan& p) {
+  if (p.I == 1) {
+    if (p.R == 16) return launch_one<BITS, XBF16, SBF16, M, 16, 1>(a, p);
+    if (p.R == 8) return launch_one<BITS, XBF16, SBF16, M, 8, 1>(a, p);
+    if (p.R == 4) return launch_one<BITS, XBF16, SBF16, M, 4, 1>(a, p);
+    return launch_one<BITS, XBF16, SBF16, M, 2, 1>(a, p);
+  }
+  if constexpr (M <= 2) {
+    if (p.I == 2) {
+      if (p.R == 4) return launch_one<BITS, XBF16, SBF16, M, 4, 2>(a, p);
+      return launch_one<BITS, XBF16, SBF16, M, 2, 2>(a, p);
+    }
+  }
+  if constexpr (M == 1) {
+    if (p.I == 3) return launch_one<BITS, XBF16, SBF16, 1, 2, 3>(a, p);
+    if (p.I == 4) return launch_one<BITS, XBF16, SBF16, 1, 2, 4>(a, p);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int BITS, bool XBF16, bool SBF16>
+hipError_t launch_s(const QmvArgs& a, const GemvPlan& p) {
+  if (a.M == 1) return launch_m<BITS, XBF16, SBF16, 1>(a, p);
+  if (a.M == 2) return launch_m<BITS, XBF16, SBF16, 2>(a, p);
+  return launch_m<BITS, XBF16, SBF16, 4>(a, p);
+}
+
+template <int BITS, bool XBF16>
+hipError_t launch_x(const QmvArgs& a, const GemvPlan& p) {
+  return a.sdt == DT_BF16 ? launch_s<BITS, XBF16, true>(a, p) : launch_s<BITS, XBF16, false>(a, p);
+}
+
+}  // namespace
+
+bool gemv_fits(int64_t M, int64_t N, int64_t K, int bits, int gs) {
+  const int64_t lim = (int64_t)1 << 31;  // byte offsets are 32-bit signed
+  return N * K * bits / 8 < lim && M * K * 2 < lim && N * (K / gs) * 2 < lim;
+}
+
+int gemv_max_m(int K, int bits) {
+  const int I = plan_gemv(1, K, bits).I;
+  return I == 1 ? 4 : (I == 2 ? 2 : (I <= 4 ? 1 : 0));
+}
+
+hipError_t launch_gemv(const QmvArgs& a) {
+  if (a.M < 1 || a.M > gemv_max_m(a.K, a.bits)) return hipErrorInvalidValue;
+  const GemvPlan p = plan_gemv(a.N, a.K, a.bits);
+  const bool xbf16 = a.xdt == DT_BF16;
+  if (a.bits == 4) return xbf16 ? launch_x<4, true>(a, p) : launch_x<4, false>(a, p);
+  return xbf16 ? launch_x<8, true>(a, p) : launch_x<8, false>(a, p);
+}
+
+}  // namespace kh

@@ -24,6 +24,14 @@ struct QmvArgs {
 // Largest M served by the decode kernel; larger M takes the prefill GEMM.
 constexpr int kDecodeMaxM = 16;
 
+// Decode GEMV for the smallest batches: VALU dot products over one pass of
+// the weights, activations held in registers. Serves 1 <= M <= gemv_max_m(K,
+// bits) (4, or fewer for very long rows; 0 when K is too long for it).
+int gemv_max_m(int K, int bits);
+// The kernel addresses each operand with 32-bit byte offsets.
+bool gemv_fits(int64_t M, int64_t N, int64_t K, int bits, int gs);
+hipError_t launch_gemv(const QmvArgs& a);
+
 // Decode path (M <= kDecodeMaxM; correct up to M = 64), MFMA on unscaled
 // codes with per-group fp32 scaling.
 hipError_t launch_qmv(const QmvArgs& a);

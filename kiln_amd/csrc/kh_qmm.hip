@@ -40,26 +40,6 @@ constexpr int BPAD = 4;     // words of padding per k-block row of the code tile
 #endif
 constexpr int PF = KH_QMM_PF;  // stages of global loads in flight
 
-// Pair order of the B operand built from packed codes; the activations are
-// permuted to match. 4-bit word -> (c0,c4)(c1,c5)(c2,c6)(c3,c7);
-// 8-bit word pair -> (c0,c2)(c1,c3)(c4,c6)(c5,c7).
-template <int BITS>
-__device__ __forceinline__ u32x4 permute_x(u32x4 d) {
-  u32x4 r;
-  if constexpr (BITS == 4) {
-    r[0] = perm(d[2], d[0], 0x05040100u);
-    r[1] = perm(d[2], d[0], 0x07060302u);
-    r[2] = perm(d[3], d[1], 0x05040100u);
-    r[3] = perm(d[3], d[1], 0x07060302u);
-  } else {
-    r[0] = perm(d[1], d[0], 0x05040100u);
-    r[1] = perm(d[1], d[0], 0x07060302u);
-    r[2] = perm(d[3], d[2], 0x05040100u);
-    r[3] = perm(d[3], d[2], 0x07060302u);
-  }
-  return r;
-}
-
 // Pairs of codes as float16 (1024 + q) in both halves (exact for q < 1024).
 template <int BITS>
 __device__ __forceinline__ void code_pairs(uint32_t q0, uint32_t q1, uint32_t mag, uint32_t* r) {

@@ -48,26 +48,6 @@
 
 namespace kh {
 
-// Pair order of the B operand built from packed codes; the activations are
-// permuted to match. 4-bit word -> (c0,c4)(c1,c5)(c2,c6)(c3,c7);
-// 8-bit word pair -> (c0,c2)(c1,c3)(c4,c6)(c5,c7).
-template <int BITS>
-__device__ __forceinline__ u32x4 permute_x(u32x4 d) {
-  u32x4 r;
-  if constexpr (BITS == 4) {
-    r[0] = perm(d[2], d[0], 0x05040100u);
-    r[1] = perm(d[2], d[0], 0x07060302u);
-    r[2] = perm(d[3], d[1], 0x05040100u);
-    r[3] = perm(d[3], d[1], 0x07060302u);
-  } else {
-    r[0] = perm(d[1], d[0], 0x05040100u);
-    r[1] = perm(d[1], d[0], 0x07060302u);
-    r[2] = perm(d[3], d[2], 0x05040100u);
-    r[3] = perm(d[3], d[2], 0x07060302u);
-  }
-  return r;
-}
-
 template <int BITS, bool XBF16>
 struct CodeOffset {
   static constexpr float value = (BITS == 8 && XBF16) ? 0.0f : (XBF16 ? 128.0f : 1024.0f);

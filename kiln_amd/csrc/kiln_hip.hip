@@ -298,17 +298,17 @@ int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
   if (M == 0 || N == 0) return KH_OK;
   if ((rc = check_device(op))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (K == 0) {
-    hipError_t e = hipMemsetAsync(res->data, 0, (size_t)(M * N * dtype_size(res->dtype)), st);
-    return e == hipSuccess ? KH_OK : hip_fail(op, e);
-  }
   kh::QmvArgs a{x->data, x->dtype, w->data, scales->data, biases->data, scales->dtype, res->data,
                 res->dtype, (int)M, (int)N, (int)K, gs, bits, st};
-  const bool fast = transpose && x->dtype != KH_FLOAT32 && scales->dtype != KH_FLOAT32 &&
+  // K == 0 takes the general kernel too: its empty sums write zeros (a
+  // kernel, not a memset, so the call stays safe under graph capture).
+  const bool fast = K > 0 && transpose && x->dtype != KH_FLOAT32 && scales->dtype != KH_FLOAT32 &&
                     aligned16(x->data) && aligned16(w->data);
   hipError_t e;
   if (!fast) {
     e = kh::launch_qmm_generic(a, transpose);
+  } else if (M <= kh::gemv_max_m((int)K, bits) && kh::gemv_fits(M, N, K, bits, gs)) {
+    e = kh::launch_gemv(a);
   } else if (M <= kh::kDecodeMaxM) {
     e = kh::launch_qmv(a);
   } else {

@@ -35,3 +35,14 @@ def parity_metrics(y: np.ndarray, ref: np.ndarray):
     ref = ref.astype(np.float64)
     err = np.abs(y - ref)
     return float(err.max() / max(np.abs(ref).max(), 1e-30)), float(err.mean() / max(np.abs(ref).mean(), 1e-30))
+
+
+def gemv_max_m(K: int, bits: int) -> int:
+    """Largest M the VALU decode GEMV serves for rows of K codes: each lane
+    slot of a workgroup of at most 8 waves owns I 16-byte chunks per row, and
+    M*I activation chunks must fit in registers (kh_gemv.hip, plan_gemv)."""
+    nch = K * bits // 128
+    I = 1
+    while -(-nch // (64 * I)) > 8:
+        I += 1
+    return 4 if I == 1 else 2 if I == 2 else 1 if I <= 4 else 0

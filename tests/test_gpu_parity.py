@@ -16,7 +16,7 @@ import torch
 from kiln_amd import ops
 from kiln_amd.workloads import make_linear_numpy, make_x_numpy
 
-from _util import dev, host, parity_metrics
+from _util import dev, gemv_max_m, host, parity_metrics
 
 pytestmark = pytest.mark.gpu
 
@@ -125,19 +125,39 @@ def test_qmm_leading_dims_and_empty(oracle):
     assert tuple(e.shape) == (0, 32)
 
 
-@pytest.mark.parametrize("bits,gs", [(4, 64), (8, 128), (4, 32)])
-def test_rows_are_m_invariant(bits, gs):
+@pytest.mark.parametrize("bits,gs,K", [(4, 64, 1024), (8, 128, 1024), (4, 32, 1024), (8, 64, 9216)])
+def test_rows_are_m_invariant(bits, gs, K):
     """Row r of the result is bitwise the same for every M served by the same
-    kernel: 1..16 (decode) and 17..N (prefill) — the property Kiln's
-    calibration probes (crates/kiln-models/src/nn.rs:301-327)."""
-    N, K = 272, 1024
+    kernel: 1..gemv_max_m (VALU decode), ..16 (MFMA decode) and 17..N
+    (prefill) — the property Kiln's calibration probes
+    (crates/kiln-models/src/nn.rs:301-327)."""
+    N = 272
     L, x = _case(200, N, K, gs, bits, seed=21)
-    dec = _run(L, x[:16], gs, bits, "bf16", "f16", "bf16")
-    for M in (1, 2, 5, 15):
-        assert np.array_equal(_run(L, x[:M], gs, bits, "bf16", "f16", "bf16"), dec[:M]), M
+    g = gemv_max_m(K, bits)
+    run = lambda M: _run(L, x[:M], gs, bits, "bf16", "f16", "bf16")
+    small = run(g)
+    for M in range(1, g):
+        assert np.array_equal(run(M), small[:M]), M
+    dec = run(16)
+    for M in sorted({g + 1, 5, 15} - set(range(g + 1))):
+        assert np.array_equal(run(M), dec[:M]), M
     pre = _run(L, x, gs, bits, "bf16", "f16", "bf16")
     for M in (17, 33, 64, 129):
-        assert np.array_equal(_run(L, x[:M], gs, bits, "bf16", "f16", "bf16"), pre[:M]), M
+        assert np.array_equal(run(M), pre[:M]), M
+
+
+# Shapes that exercise every VALU-decode plan: I = 1..4 chunks per lane slot,
+# chunk counts that leave lane slots idle, N not a multiple of the rows per
+# workgroup, M = 3 through the M = 4 kernel, f16 activations, bf16 scales.
+@pytest.mark.parametrize("N,K,bits,gs", [(37, 4096, 4, 64), (1000, 3584, 8, 32), (21, 14336, 4, 128),
+                                         (19, 20480, 4, 64), (11, 18944, 8, 128), (9, 33792, 8, 64),
+                                         (7, 65536, 4, 32), (130, 96, 4, 32), (64, 2048, 8, 64)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("xdt,sdt", [("bf16", "f16"), ("f16", "bf16")])
+def test_gemv_plans(oracle, N, K, bits, gs, M, xdt, sdt):
+    L, x = _case(M, N, K, gs, bits, xdt=xdt, sdt=sdt, seed=N + K + M)
+    y = _run(L, x, gs, bits, xdt, sdt, "f32")
+    _check_f32(oracle, L, x, gs, bits, xdt, sdt, y.view(np.float32), rel=EXACT_REL)
 
 
 @pytest.mark.parametrize("path", sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz")))
