@@ -1,23 +1,26 @@
 """Benchmark of the affine-quantized linear path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload llama-3-8b]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-sweep]
 
-Workload: the seven Llama-3-8B decoder linears
-(q/k/v/o 4096x4096|1024x4096, gate/up 14336x4096, down 4096x14336), 4-bit
-codes, group size 64, fp16 scales/biases, bf16 activations ~N(0,1), bf16
-output, random-init (synthetic) weights generated in HBM.
+Headline (the JSON line's `value`): BASELINE configs[2], the seven
+Llama-3-8B decoder linears (q/k/v/o 4096x4096|1024x4096, gate/up
+14336x4096, down 4096x14336), 4-bit codes, group size 64, fp16
+scales/biases, bf16 activations ~N(0,1), bf16 output, random-init
+(synthetic) weights generated in HBM. A step is one decode pass of one
+layer: the seven quantized_matmul calls at M = 1 through the C ABI
+(kh_quantized_matmul), replayed from a HIP graph. Steps rotate over enough
+distinct layer copies (> 512 MB) that the 256 MB MALL cannot serve the
+weights: every call reads its weights from HBM.
 
-A step is one decode pass of one layer: the seven quantized_matmul calls at
-M = 1, each through the C ABI (kh_quantized_matmul). Steps rotate over
-enough distinct layer copies (> 512 MB) that the 256 MB MALL cannot serve
-the weights; every call reads its weights from HBM.
-
-value = whole-step algorithmic bytes / step time (GB/s) at M = 1.
-roofline = the dominant kernel (the decode GEMV at gate/up shape): algorithmic
-bytes per launch / its average launch duration, measured with HIP events on
-the stream the library launches on.
-Also reported: prefill (M = 2048) dequant-GEMM TFLOP/s over the seven
-linears, and the CPU baseline (the oracle's C restatement, OpenMP).
+value    = whole-step algorithmic bytes / step time (GB/s), bytes per call
+           N*K*bits/8 + 2*N*(K/gs)*2 + M*K*2 + M*N*2.
+roofline = the dominant kernel (decode GEMV at gate 14336x4096): its
+           algorithmic bytes per launch / its average launch duration, from
+           HIP events on the stream the library launches on.
+sweep    = every BASELINE configuration: per-layer (or per-call) time, GB/s
+           and TFLOP/s for each M the configuration lists.
+cpu_baseline = the oracle's C restatement (OpenMP, float32 accumulate) on
+           the host cores over the same M = 1 step, for about --cpu-seconds.
 """
 from __future__ import annotations
 
@@ -32,23 +35,22 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 600_000_000  # rotate over more distinct weight bytes than the 256 MB MALL
 
 
-def layer_bytes(N, K, M, bits=4, gs=64):
-    """Algorithmic bytes of one call: packed codes + fp16 scales and biases +
-    bf16 activations + bf16 output."""
+def call_bytes(N, K, M, bits, gs):
+    """Algorithmic bytes of one call: packed codes + 16-bit scales and
+    biases + bf16 activations + bf16 output."""
     return N * K * bits // 8 + 2 * N * (K // gs) * 2 + M * K * 2 + M * N * 2
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="llama-3-8b")
-    ap.add_argument("--prefill-m", type=int, default=2048)
-    ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -64,131 +66,80 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    gs, bits = 64, 4
-    shapes = LAYER_SHAPES[args.workload]
-    per_layer = sum(N * K // 2 for _, N, K in shapes)
-    copies = max(2, -(-600_000_000 // per_layer))  # > 512 MB of distinct weights
-    layers = []
-    for c in range(copies):
-        layers.append({name: make_linear_device(N, K, gs, "q4", seed=1000 * c + i, device=dev)
-                       for i, (name, N, K) in enumerate(shapes)})
-    g = torch.Generator(device=dev).manual_seed(7)
-    xs = {K: torch.randn((1, K), generator=g, device=dev).bfloat16() for _, _, K in shapes}
-    outs = {name: torch.empty((1, N), dtype=torch.bfloat16, device=dev) for name, N, _ in shapes}
     stream = torch.cuda.current_stream(dev)
+    g = torch.Generator(device=dev).manual_seed(7)
 
-    def step(i):
-        L = layers[i % copies]
-        for name, N, K in shapes:
-            W = L[name]
-            ops.quantized_matmul(xs[K], W["w"], W["scales"], W["biases"], True, gs, bits,
-                                 out=outs[name])
+    def layer_copies(shapes, gs, dist, copies=None):
+        bits = 4 if dist != "q8" else 8
+        per = sum(N * K * bits // 8 for _, N, K in shapes)
+        copies = copies or max(2, -(-MALL_BYTES // per))
+        return [{name: make_linear_device(N, K, gs, dist, seed=1000 * c + i, device=dev)
+                 for i, (name, N, K) in enumerate(shapes)} for c in range(copies)]
 
-    def capture(fn):
-        """Record fn's launches (made on torch's current stream, which is the
-        capture stream inside the context) into a HIP graph."""
+    def graph_us(fn, copies, reps):
+        """Average µs of fn(c) over a graph holding fn(0..copies-1), replayed
+        `reps` times; HIP events on the capture/replay stream."""
+        for c in range(copies):
+            fn(c)
+        torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            fn()
-        return graph
-
-    # Eager warm-up, then one graph holding `copies` decode steps (one per
-    # weight copy) so a replay walks > 512 MB of distinct weights.
-    for i in range(copies):
-        step(i)
-    torch.cuda.synchronize()
-    g_step = capture(lambda: [step(i) for i in range(copies)])
-    reps = max(1, -(-args.steps // copies))
-    wreps = max(1, -(-args.warmup // copies))
-    for _ in range(wreps):
-        g_step.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        g_step.replay()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    nsteps = reps * copies
-    ms_per_step = wall * 1e3 / nsteps
-    step_bytes = sum(layer_bytes(N, K, 1, bits, gs) for _, N, K in shapes)
-    value = step_bytes / (wall / nsteps) / 1e9
-
-    # Per-launch duration of each shape: a graph of that shape's launches over
-    # every weight copy, bracketed by HIP events recorded on the replay stream.
-    stream = torch.cuda.current_stream(dev)
-    per_shape_us = {}
-    for name, N, K in shapes:
-        def one_shape(name=name, K=K):
-            for i in range(copies):
-                W = layers[i][name]
-                ops.quantized_matmul(xs[K], W["w"], W["scales"], W["biases"], True, gs, bits,
-                                     out=outs[name])
-        gr = capture(one_shape)
-        gr.replay()
+            for c in range(copies):
+                fn(c)
+        graph.replay()
+        torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
-        nrep = 20
         e0.record(stream)
-        for _ in range(nrep):
-            gr.replay()
+        for _ in range(reps):
+            graph.replay()
         e1.record(stream)
         torch.cuda.synchronize()
-        per_shape_us[name] = 1e3 * e0.elapsed_time(e1) / (nrep * copies)
-    dom = "gate"
-    dN, dK = next((N, K) for n, N, K in shapes if n == dom)
-    dom_us = per_shape_us[dom]
-    dom_bytes = layer_bytes(dN, dK, 1, bits, gs)
+        us = 1e3 * e0.elapsed_time(e1) / (reps * copies)
+        del graph
+        return us
+
+    def layer_fns(layers, shapes, M, gs, bits):
+        xs = {K: torch.randn((M, K), generator=g, device=dev).bfloat16() for _, _, K in shapes}
+        outs = {name: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for name, N, _ in shapes}
+
+        def one(name, K):
+            def f(c):
+                W = layers[c][name]
+                ops.quantized_matmul(xs[K], W["w"], W["scales"], W["biases"], True, gs, bits,
+                                     out=outs[name])
+            return f
+
+        per = {name: one(name, K) for name, _, K in shapes}
+
+        def step(c):
+            for name, _, _ in shapes:
+                per[name](c)
+        return step, per
+
+    # ---------------- headline: Llama-3-8B decode step at M = 1
+    gs, bits = 64, 4
+    shapes = LAYER_SHAPES["llama-3-8b"]
+    layers = layer_copies(shapes, gs, "q4")
+    copies = len(layers)
+    step, per = layer_fns(layers, shapes, 1, gs, bits)
+    reps = max(1, -(-args.steps // copies))
+    wreps = max(1, -(-args.warmup // copies))
+    graph_us(step, copies, wreps)  # warm-up
+    step_us = graph_us(step, copies, reps)
+    nsteps = reps * copies
+    step_bytes = sum(call_bytes(N, K, 1, bits, gs) for _, N, K in shapes)
+    value = step_bytes / (step_us * 1e-6) / 1e9
+    per_shape_us = {name: graph_us(per[name], copies, 20) for name, _, _ in shapes}
+    dN, dK = next((N, K) for n, N, K in shapes if n == "gate")
+    dom_us = per_shape_us["gate"]
+    dom_bytes = call_bytes(dN, dK, 1, bits, gs)
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
-    per_shape_gbs = {n: round(layer_bytes(N, K, 1, bits, gs) / (per_shape_us[n] * 1e-6) / 1e9, 1)
-                     for n, N, K in shapes}
-    per_shape_us = {n: round(v, 2) for n, v in per_shape_us.items()}
 
-    # Prefill: the seven linears at M = prefill_m, MFMA dequant-GEMM path.
-    Mp = args.prefill_m
-    xp = {K: torch.randn((Mp, K), generator=g, device=dev).bfloat16() for _, _, K in shapes}
-    op = {name: torch.empty((Mp, N), dtype=torch.bfloat16, device=dev) for name, N, _ in shapes}
+    sweep = {} if args.no_sweep else run_sweep(torch, ops, layers, shapes, graph_us, layer_fns,
+                                               layer_copies, make_linear_device, dev, g)
 
-    def pstep(i, events=None):
-        L = layers[i % copies]
-        for name, N, K in shapes:
-            W = L[name]
-            if events is not None:
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-            ops.quantized_matmul(xp[K], W["w"], W["scales"], W["biases"], True, gs, bits,
-                                 out=op[name])
-            if events is not None:
-                e1.record(stream)
-                events.append((name, e0, e1))
-
-    for i in range(2):
-        pstep(i)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.prefill_steps):
-        pstep(i)
-    torch.cuda.synchronize()
-    pwall = (time.perf_counter() - t0) / args.prefill_steps
-    flops = sum(2 * Mp * N * K for _, N, K in shapes)
-    pevents = []
-    for i in range(args.prefill_steps):
-        pstep(i, pevents)
-    torch.cuda.synchronize()
-    pgate = [e0.elapsed_time(e1) for n, e0, e1 in pevents if n == dom]
-    pgate_ms = sum(pgate) / len(pgate)
-    prefill = {
-        "m": Mp,
-        "tflops": round(flops / pwall / 1e12, 1),
-        "ms_per_layer": round(pwall * 1e3, 3),
-        "gate_tflops": round(2 * Mp * dN * dK / (pgate_ms * 1e-3) / 1e12, 1),
-        "gate_us": round(pgate_ms * 1e3, 1),
-        "frac_of_bf16_peak": round(flops / pwall / 1e12 / BF16_PEAK_TFLOPS, 4),
-    }
-
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(shapes, gs, bits, args.cpu_seconds)
+    cpu = None if args.no_cpu else cpu_baseline(shapes, gs, bits, args.cpu_seconds)
 
     line = {
         "metric": "q4 GEMV HBM GB/s (% of peak) at M=1; dequant-GEMM TFLOP/s at M=2048",
@@ -196,34 +147,114 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": nsteps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "warmup": wreps * copies,
+        "ms_per_step": round(step_us * 1e-3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u4 codes, bf16 activations, fp32 accumulate",
         "data": "synthetic (seeded random codes/scales/biases in HBM, x ~ N(0,1))",
-        "config": {"workload": f"{args.workload} decoder linears (q,k,v,o,gate,up,down), 4-bit gs64, M=1 decode step",
+        "config": {"workload": "llama-3-8b decoder linears (q,k,v,o,gate,up,down), 4-bit gs64, M=1 "
+                               "decode step (BASELINE configs[2])",
                    "m": 1, "group_size": gs, "bits": bits, "weight_copies": copies,
-                   "weight_bytes_rotated": copies * per_layer},
+                   "weight_bytes_rotated": copies * sum(N * K // 2 for _, N, K in shapes)},
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "qmv_kernel<4,64,bf16,1> at gate 14336x4096",
+                     "kernel": "gemv_kernel<4,bf16,f16,M=1,R=8,I=1> at gate 14336x4096",
                      "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 3)},
-        "per_shape_us": per_shape_us,
-        "per_shape_gbs": per_shape_gbs,
-        "prefill": prefill,
+        "per_shape_us": {k: round(v, 2) for k, v in per_shape_us.items()},
+        "per_shape_gbs": {n: round(call_bytes(N, K, 1, bits, gs) / (per_shape_us[n] * 1e-6) / 1e9, 1)
+                          for n, N, K in shapes},
+        "prefill_m2048_tflops": sweep.get("llama-3-8b", {}).get("prefill", {}).get("2048", {}).get("tflops"),
+        "sweep": sweep,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
 
+def run_sweep(torch, ops, l8_layers, l8_shapes, graph_us, layer_fns, layer_copies, make_linear_device,
+              dev, g):
+    """Every BASELINE configuration, one entry per M; per-layer figures sum the
+    seven linears of one layer, replayed from a graph over > 512 MB of weights."""
+    from kiln_amd.workloads import LAYER_SHAPES
+
+    def entry(shapes, M, gs, bits, us):
+        b = sum(call_bytes(N, K, M, bits, gs) for _, N, K in shapes)
+        f = sum(2 * M * N * K for _, N, K in shapes)
+        return {"us": round(us, 2), "gbs": round(b / (us * 1e-6) / 1e9, 1),
+                "tflops": round(f / (us * 1e-6) / 1e12, 2)}
+
+    def measure(layers, shapes, Ms, gs, bits, reps_for):
+        res = {}
+        for M in Ms:
+            step, _ = layer_fns(layers, shapes, M, gs, bits)
+            us = graph_us(step, len(layers), reps_for(M))
+            res[str(M)] = entry(shapes, M, gs, bits, us)
+            print(f"# sweep {shapes[0][1]}x{shapes[0][2]}.. M={M}: {res[str(M)]}", file=sys.stderr,
+                  flush=True)
+        return res
+
+    out = {}
+    # configs[2]: Llama-3-8B, decode M in {1,8,32,64}, prefill M in {512,2048,4096}
+    out["llama-3-8b"] = {"decode": measure(l8_layers, l8_shapes, (1, 8, 32, 64), 64, 4, lambda M: 20),
+                         "prefill": measure(l8_layers[:2], l8_shapes, (512, 2048, 4096), 64, 4,
+                                            lambda M: 3)}
+    pf = out["llama-3-8b"]["prefill"]["2048"]
+    pf["frac_of_bf16_peak"] = round(pf["tflops"] / BF16_PEAK_TFLOPS, 4)
+
+    # configs[0]: one 8192x2048 matvec
+    s0 = [("w", 8192, 2048)]
+    L0 = layer_copies(s0, 64, "q4", copies=80)
+    out["cfg0-8192x2048"] = measure(L0, s0, (1,), 64, 4, lambda M: 20)
+    del L0
+
+    # configs[1]: Llama-3.2-1B, M in {1,4,16,32}, per layer and x16 layers
+    s1 = LAYER_SHAPES["llama-3.2-1b"]
+    L1 = layer_copies(s1, 64, "q4")
+    r1 = measure(L1, s1, (1, 4, 16, 32), 64, 4, lambda M: 20)
+    for v in r1.values():
+        v["us_16_layers"] = round(16 * v["us"], 1)
+    out["llama-3.2-1b"] = r1
+    del L1
+
+    # configs[3]: Qwen2.5-7B 8-bit, gs 32 and 128, M in {1,16,2048}
+    s3 = LAYER_SHAPES["qwen2.5-7b"]
+    for gs3 in (32, 128):
+        L3 = layer_copies(s3, gs3, "q8")
+        r = measure(L3, s3, (1, 16), gs3, 8, lambda M: 10)
+        r.update(measure(L3[:2], s3, (2048,), gs3, 8, lambda M: 3))
+        out[f"qwen2.5-7b-q8-gs{gs3}"] = r
+        del L3
+
+    # configs[4]: tied head 128256x4096 4-bit gs128 at M in {1,32,256}; gather of 4096 Zipf ids
+    s4 = [("head", 128256, 4096)]
+    L4 = layer_copies(s4, 128, "emb")
+    out["lm-head-128256x4096-gs128"] = measure(L4, s4, (1, 32, 256), 128, 4, lambda M: 10)
+    import numpy as np
+    rng = np.random.default_rng(4000)
+    ids = []
+    while len(ids) < 4096:
+        z = rng.zipf(1.1, 8192) - 1
+        ids.extend(int(v) for v in z[z < 128256])
+    idt = torch.tensor(ids[:4096], dtype=torch.int32, device=dev).view(torch.int32)
+    H, T = 4096, 4096
+    eo = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+
+    def gather(c):
+        W = L4[c]["head"]
+        ops.quantized_embedding(idt, W["w"], W["scales"], W["biases"], 128, 4, out=eo)
+
+    us = graph_us(gather, len(L4), 20)
+    eb = T * (H * 4 // 8 + 2 * (H // 128) * 2 + 2 * H) + 4 * T
+    out["embedding-gather-4096-zipf"] = {"us": round(us, 2), "gbs": round(eb / (us * 1e-6) / 1e9, 1)}
+    del L4
+    return out
+
+
 def cpu_baseline(shapes, gs, bits, seconds):
     """The oracle's C restatement (OpenMP, float32 accumulate) over the same
     decode step on host cores, repeated for about `seconds`."""
-    import numpy as np
-
     from kiln_amd.workloads import make_linear_numpy, make_x_numpy
     from oracle import oracle
 
@@ -237,12 +268,11 @@ def cpu_baseline(shapes, gs, bits, seconds):
     while True:
         for N, K, L, x in data:
             oracle.quantized_matmul(x, "bf16", L["w"], L["scales"], L["biases"], "f16", gs, bits, True, "bf16")
-            nbytes += layer_bytes(N, K, 1, bits, gs)
+            nbytes += call_bytes(N, K, 1, bits, gs)
         reps += 1
         if time.perf_counter() - t0 >= seconds:
             break
     dt = time.perf_counter() - t0
-    del np
     return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": int(oracle.lib().kho_threads()),
             "kind": "port",
             "sample": f"{reps} x the 7-linear M=1 decode step (same shapes), oracle/kh_oracle.c kho_qmm, "
