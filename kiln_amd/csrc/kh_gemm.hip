@@ -1,0 +1,439 @@
+// kh_gemm.hip — quantized GEMM for gfx950, every M above the VALU-GEMV range.
+//
+// y[m, n] = sum_k x[m, k] * w[n, k], w = s[n, g(k)] * q[n, k] + b[n, g(k)]
+// (quantized_matmul, transpose=true: crates/kiln-mlx/src/ops.rs:359-388).
+//
+// Numerics: as the prefill path of kh_qmm.hip. qmm_prep_x has written x as
+// float16 rows scaled by an exact power of two (rscale = 2^e_m), permuted
+// into the pair order of the code operand. Each weight is dequantised once,
+// in registers, to float16 with one rounding, w16 = fma16(s, q, b), and the
+// products accumulate in float32 (v_mfma_f32_16x16x32_f16). Outputs are
+// multiplied back by rscale.
+//
+// Work decomposition. A workgroup of four waves owns a (16*MT) x 256 output
+// tile and one K slice; the waves split N (64 columns each, four 16-column
+// MFMA tiles), so every weight is dequantised exactly once. K is walked in
+// stages of 128 codes:
+//   - codes go from HBM straight into registers in MFMA operand layout
+//     (lane (n, lg) holds 16 bytes of row n: one load per 16-row tile at 4
+//     bits, two at 8 bits), prefetched two stages ahead;
+//   - the activation tile of the stage (16*MT rows x 128 k, float16) is
+//     copied HBM/L2 -> LDS by the direct global-to-LDS loads of gfx950 (each
+//     instruction four whole rows, 1 KB contiguous), into a ring of LDS
+//     buffers, row-major with the 16-byte blocks XOR-swizzled by row so the
+//     MFMA operand reads are free of bank conflicts;
+//   - one barrier per stage.
+// K slices (split-K, chosen from N, K and M-tiles only) write float32
+// partials that gemm_reduce sums in slice order, so results are
+// deterministic. Tiles are ordered so that the workgroups resident on one
+// XCD share the activation panel in that XCD's L2.
+#include "kh_common.h"
+#include "kh_kernels.h"
+
+namespace kh {
+
+namespace {
+
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 h2;
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kStage = 128;   // codes per K stage
+constexpr int kWaves = 4;
+constexpr int kNT = 4;        // 16-column tiles per wave
+constexpr int kBN = kWaves * kNT * 16;  // 256
+constexpr int kXcds = 8;
+constexpr int kMaxMT = 8;     // largest m tile: 128 rows
+
+// s_waitcnt vmcnt(N) leaving expcnt and lgkmcnt unconstrained (gfx9
+// encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
+template <int N>
+__device__ __forceinline__ void waitcnt_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+__device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Pairs of codes as float16 (1024 + q) in both halves (exact for q < 1024),
+// in the pair order of permute_x: 4-bit word -> (c0,c4)(c1,c5)(c2,c6)(c3,c7);
+// 8-bit word pair -> (c0,c2)(c1,c3)(c4,c6)(c5,c7).
+template <int BITS>
+__device__ __forceinline__ void pairs_1024(uint32_t q0, uint32_t q1, uint32_t mag, uint32_t* r) {
+  if constexpr (BITS == 4) {
+    r[0] = (q0 & 0x000f000fu) | mag;
+    r[1] = ((q0 >> 4) & 0x000f000fu) | mag;
+    r[2] = ((q0 >> 8) & 0x000f000fu) | mag;
+    r[3] = ((q0 >> 12) & 0x000f000fu) | mag;
+  } else {
+    r[0] = (q0 & 0x00ff00ffu) | mag;
+    r[1] = ((q0 >> 8) & 0x00ff00ffu) | mag;
+    r[2] = (q1 & 0x00ff00ffu) | mag;
+    r[3] = ((q1 >> 8) & 0x00ff00ffu) | mag;
+  }
+}
+
+// 16-bit scale/bias halves -> (v, v) float16 pair. bf16 values are converted
+// through float32 to float16 (round to nearest even); scales and biases of
+// the supported formats are far inside float16's normal range.
+template <bool SF16>
+__device__ __forceinline__ h2 half_pair(uint32_t h) {
+  if constexpr (SF16) {
+    return __builtin_bit_cast(h2, h | (h << 16));
+  } else {
+    const _Float16 v = (_Float16)bf16_bits_to_f32(h);
+    return h2{v, v};
+  }
+}
+
+// Offset (codes) of the 8-code block lane group lg contributes to MFMA step j
+// of a stage: 4-bit lanes hold 32 consecutive codes (16 bytes), step j takes
+// word j; 8-bit lanes hold two 16-code runs 64 apart, step j takes words
+// 2(j%2), 2(j%2)+1 of run j/2.
+template <int BITS>
+__device__ __forceinline__ int step_off(int j, int lg) {
+  return BITS == 4 ? lg * 32 + 8 * j : (j >> 1) * 64 + lg * 16 + (j & 1) * 8;
+}
+
+// Stages kept in flight: deep for small tiles (the launch is latency-bound),
+// shallower where registers and LDS go to the accumulator tile.
+#ifndef KH_GEMM_NT
+#define KH_GEMM_NT 1  // code loads marked non-temporal
+#endif
+#ifndef KH_GEMM_ABL
+#define KH_GEMM_ABL 0  // tuning ablations: 1 no dequant/MFMA, 2 no scale loads, 3 no activation DMA/barrier
+#endif
+#ifndef KH_GEMM_P
+#define KH_GEMM_P 0   // tuning: force the ring depth (0 = by tile size)
+#endif
+constexpr int ring_depth(int bits, int mt) {
+  return KH_GEMM_P ? KH_GEMM_P : (mt <= 2 ? 4 : 2);
+}
+
+// Scale/bias chunk: the groups of P stages (P*128 codes) of every row of the
+// workgroup, copied to LDS by direct loads of SPIECE bytes.
+template <int GS, int P>
+struct ScaleChunk {
+  static constexpr int GC = P * kStage / GS;            // groups per row
+  static constexpr int BYTES = GC * 2;                  // per row and array
+  // A piece never spans two stages (a stage is 2*128/GS bytes of a row), so
+  // each piece lies wholly inside the row's groups or wholly past its end —
+  // the row's valid groups end on a stage boundary.
+  static constexpr int SPIECE = GS == 128 ? 2 : 4;      // direct-load size
+  static constexpr int PIECES = BYTES / SPIECE;         // per row and array
+  static_assert(PIECES * SPIECE == BYTES && (2 * kStage / GS) % SPIECE == 0, "pieces tile stages");
+  // Direct loads of fewer than 4 bytes still write one dword per lane in LDS.
+  static constexpr int SSTRIDE = SPIECE < 4 ? 4 : SPIECE;     // LDS bytes per piece
+  static constexpr int LDS_BYTES = 2 * kBN * PIECES * SSTRIDE;  // one chunk buffer
+  // LDS byte offset of group g (within the chunk) of row `row`, array `arr`
+  __device__ static constexpr int offset(int arr, int row, int g) {
+    return ((arr * kBN + row) * PIECES + g / (SPIECE / 2)) * SSTRIDE + (g % (SPIECE / 2)) * 2;
+  }
+  static constexpr int OPS = 2 * kBN * PIECES / (64 * kWaves);  // direct loads per lane
+};
+
+template <int BITS, bool SF16, int MT, int GS>
+__global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
+    const u32x4* __restrict__ xh, const float* __restrict__ rscale,
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ biases, float* __restrict__ part, void* __restrict__ out,
+    int odt, int M, int N, int K, int kslice, int tiles_n, int tiles_m, int nsplit) {
+  constexpr int BM = 16 * MT;
+  constexpr int LW = BITS / 4;             // 16-byte code loads per lane per 16-row tile
+  constexpr int SLOTS = 16 * BM;           // u32x4 activation slots per stage
+  constexpr int DOPS = (SLOTS + 64 * kWaves - 1) / (64 * kWaves);  // activation loads per lane
+  constexpr int P = ring_depth(BITS, MT);  // stages in flight
+  using SC = ScaleChunk<GS, P>;
+  constexpr int LGS = __builtin_ctz(GS);
+
+  __shared__ u32x4 As[P][SLOTS];
+  __shared__ __align__(16) unsigned char Ss[2][SC::LDS_BYTES];  // [chunk buf][scales|biases][row][piece]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, lg = lane >> 4;
+
+  // XCD-aware tile order: workgroup b runs on XCD b % 8; the tiles of one XCD
+  // are consecutive in (split, m-tile, n-tile) order, n fastest.
+  const int total = tiles_n * tiles_m * nsplit;
+  const int per = (total + kXcds - 1) / kXcds;
+  const int t = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  if (t >= total) return;
+  const int tn = t % tiles_n;
+  const int tm = (t / tiles_n) % tiles_m;
+  const int sp = t / (tiles_n * tiles_m);
+
+  const int m0 = tm * BM, n0 = tn * kBN;
+  const int k0 = sp * kslice;
+  const int k1 = min(K, k0 + kslice);
+  const int nst = (k1 - k0) / kStage;      // K and kslice are multiples of kStage
+  const int G = K >> LGS;
+  const int KB8 = K / 8;
+  const int wpr = K * BITS / 32;           // words per row
+  const int nchunks = (nst + P - 1) / P;
+
+  // Rows of this lane's four code tiles (clamped: every load in bounds).
+  int nrow[kNT];
+#pragma unroll
+  for (int u = 0; u < kNT; ++u) {
+    const int n = n0 + wave * 64 + u * 16 + col;
+    nrow[u] = n < N ? n : N - 1;
+  }
+
+  // ---- loaders (all in bounds: indices past the slice or the matrix are
+  // clamped; what they fetch is never used)
+  auto load_codes = [&](u32x4 (&q)[kNT][LW], int st) {
+    const int kc = k0 + st * kStage;
+#pragma unroll
+    for (int u = 0; u < kNT; ++u) {
+      const uint32_t* row = w + (int64_t)nrow[u] * wpr;
+#pragma unroll
+      for (int h = 0; h < LW; ++h) {
+        const int code = kc + (BITS == 4 ? lg * 32 : h * 64 + lg * 16);
+        const u32x4* src = reinterpret_cast<const u32x4*>(row + code * BITS / 32);
+        q[u][h] = KH_GEMM_NT ? __builtin_nontemporal_load(src) : *src;
+      }
+    }
+  };
+  // Activation tile of a stage: row m's 16 blocks of 8 codes (256 bytes) at
+  // slots m*16 + (kb ^ (m & 15)). One direct load fills 64 consecutive slots:
+  // four whole rows, 1 KB of contiguous global memory; the XOR spreads the
+  // 16 rows an MFMA operand read touches (same kb) over all LDS banks.
+  auto load_acts = [&](int buf, int st) {
+    const int kc8 = (k0 + st * kStage) >> 3;
+#pragma unroll
+    for (int d = 0; d < DOPS; ++d) {
+      const int s = (d * kWaves + wave) * 64 + lane;
+      const int sl = s < SLOTS ? s : SLOTS - 1;
+      const int m = sl >> 4, kb = (sl & 15) ^ (m & 15);
+      const int mm = m0 + m < M ? m0 + m : M - 1;
+      if (KH_GEMM_ABL != 3 && (d * kWaves + wave) * 64 < SLOTS)  // wave-uniform
+        __builtin_amdgcn_global_load_lds(
+            (const void*)(xh + (int64_t)mm * KB8 + kc8 + kb),
+            (lds_void*)&As[buf][(d * kWaves + wave) * 64], 16, 0, 0);
+    }
+  };
+  // Scale/bias chunk c into buffer c & 1: lane op i = (array, row, piece),
+  // consecutive lanes -> consecutive pieces of one row (contiguous memory).
+  auto load_scales = [&](int c) {
+    const int g0 = (k0 >> LGS) + c * SC::GC;
+#pragma unroll
+    for (int d = 0; d < SC::OPS; ++d) {
+      const int i = (d * kWaves + wave) * 64 + lane;
+      const int piece = i % SC::PIECES, row = (i / SC::PIECES) % kBN, arr = i / (SC::PIECES * kBN);
+      const int n = n0 + row < N ? n0 + row : N - 1;
+      // a piece past the row's last group (only in the last chunk of a slice
+      // whose stage count is not a multiple of P, or past K) reads the
+      // row's last piece instead: in bounds, never used
+      const int gp = min(g0 + piece * (SC::SPIECE / 2), G - SC::SPIECE / 2);
+      const uint16_t* src = (arr ? biases : scales) + (int64_t)n * G + gp;
+      lds_void* dst = (lds_void*)&Ss[c & 1][((d * kWaves + wave) * 64) * SC::SSTRIDE];
+      if (KH_GEMM_ABL != 2) {
+        __builtin_amdgcn_global_load_lds((const void*)src, dst, SC::SPIECE, 0, 0);
+      }
+    }
+  };
+
+  uint32_t mag = 0x64006400u;  // float16 1024.0 in both halves
+  asm volatile("" : "+v"(mag));
+  const h2 k1024 = h2{(_Float16)1024.f, (_Float16)1024.f};
+
+  f32x4 acc[MT][kNT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int u = 0; u < kNT; ++u) acc[i][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 q[P][kNT][LW];  // code ring: slot p holds stage st with st % P == p
+
+  // Issue order of vector-memory ops: scales(chunk 0); for t = 0..P-2:
+  // activations(t), codes(t); then per stage st (p = st % P): wait for
+  // activations(st), barrier (the buffers and slots of stage st-1, and at a
+  // chunk start the scale buffer of chunk c-1, are free), activations(st+P-1),
+  // scales(chunk c+1) if p == 0, codes(st+P-1), arithmetic of st. Clamped
+  // indices keep this sequence free of branches, so the ops issued after
+  // activations(st) are codes(st), P-2 stages of (activations, codes), and one
+  // scale chunk unless p == 0: a compile-time count per p.
+  constexpr int OPS = LW * kNT;
+  constexpr int BASE = OPS + (P - 2) * (DOPS + OPS);
+  static_assert(BASE + SC::OPS < 64, "vmcnt holds 6 bits");
+  load_scales(0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 0; t < P - 1; ++t) {
+    load_acts(t, min(t, nst - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    load_codes(q[t], min(t, nst - 1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  for (int c = 0; c < nchunks; ++c) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int st = c * P + p;
+      if (p == 0)
+        waitcnt_vm<BASE>();
+      else
+        waitcnt_vm<BASE + SC::OPS>();
+      if (KH_GEMM_ABL != 3) __builtin_amdgcn_s_barrier();
+      const int pn = (p + P - 1) % P;  // slot and buffer of stage st + P - 1 (constant once unrolled)
+      load_acts(pn, min(st + P - 1, nst - 1));
+      if (p == 0) load_scales(min(c + 1, nchunks - 1));
+      load_codes(q[pn], min(st + P - 1, nst - 1));
+      // The waits above rely on program order of the vector memory ops.
+      __builtin_amdgcn_sched_barrier(0);
+      if (KH_GEMM_ABL == 1 && st < nst) {
+#pragma unroll
+        for (int u = 0; u < kNT; ++u)
+          acc[0][u][0] += __uint_as_float((q[p][u][0][0] ^ q[p][u][LW - 1][3]) & 0x3fffffffu) +
+                          (float)Ss[c & 1][u * 16 + col];
+      } else if (st < nst) {  // uniform
+        const unsigned char* sbuf = &Ss[c & 1][0];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          u32x4 b[kNT];
+#pragma unroll
+          for (int u = 0; u < kNT; ++u) {
+            const int h = BITS == 4 ? 0 : (j >> 1);
+            const uint32_t q0 = BITS == 4 ? q[p][u][0][j] : q[p][u][h][(j & 1) * 2];
+            const uint32_t q1 = BITS == 4 ? 0u : q[p][u][h][(j & 1) * 2 + 1];
+            uint32_t r[4];
+            pairs_1024<BITS>(q0, q1, mag, r);
+            // group of this lane's codes within the chunk
+            const int gl = (p * kStage + (BITS == 4 ? lg * 32 : h * 64 + lg * 16)) >> LGS;
+            const int row = wave * 64 + u * 16 + col;
+            const uint32_t sh = *reinterpret_cast<const uint16_t*>(sbuf + SC::offset(0, row, gl));
+            const uint32_t bh = *reinterpret_cast<const uint16_t*>(sbuf + SC::offset(1, row, gl));
+            const h2 s2 = KH_GEMM_ABL == 2 ? h2{(_Float16)0.01f, (_Float16)0.01f} : half_pair<SF16>(sh);
+            const h2 b2 = KH_GEMM_ABL == 2 ? h2{(_Float16)-0.08f, (_Float16)-0.08f} : half_pair<SF16>(bh);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              b[u][e] = __builtin_bit_cast(
+                  uint32_t, __builtin_elementwise_fma(s2, __builtin_bit_cast(h2, r[e]) - k1024, b2));
+          }
+#pragma unroll
+          for (int i = 0; i < MT; ++i) {
+            const int m = i * 16 + col, kb = step_off<BITS>(j, lg) >> 3;
+            const u32x4 a = As[p][m * 16 + (kb ^ (m & 15))];
+#pragma unroll
+            for (int u = 0; u < kNT; ++u) acc[i][u] = mfma_f16(a, b[u], acc[i][u]);
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- epilogue: D lane l holds column l%16, rows 4*(l/16)+i
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = m0 + i * 16 + 4 * lg + e;
+      if (m >= M) continue;
+      const float rs = rscale[m];
+#pragma unroll
+      for (int u = 0; u < kNT; ++u) {
+        const int n = n0 + wave * 64 + u * 16 + col;
+        if (n >= N) continue;
+        const float v = acc[i][u][e] * rs;
+        if (nsplit == 1)
+          store_from_f32(out, odt, (int64_t)m * N + n, v);
+        else
+          part[((int64_t)sp * M + m) * N + n] = v;
+      }
+    }
+  }
+}
+
+// out[m, n] = sum over slices s (in order) of part[s, m, n].
+__global__ void gemm_reduce(const float* __restrict__ part, void* __restrict__ out, int odt,
+                            int64_t MN, int nsplit) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= MN) return;
+  float s = part[i];
+  for (int k = 1; k < nsplit; ++k) s += part[(int64_t)k * MN + i];
+  store_from_f32(out, odt, i, s);
+}
+
+}  // namespace
+
+GemmPlan plan_gemm(int M, int N, int K, int bits) {
+  (void)bits;
+  GemmPlan p;
+  int mt = 1;
+  while (mt < kMaxMT && 16 * mt < M) mt *= 2;
+  p.mt = mt;
+  p.tiles_m = (M + 16 * mt - 1) / (16 * mt);
+  p.tiles_n = (N + kBN - 1) / kBN;
+  // Split K while the launch has fewer than ~2 workgroups per CU and each
+  // slice keeps at least 4 stages. Below the largest tile the split depends
+  // on (N, K, mt) only, so rows do not change with M inside one mt class.
+  const int stages = K / kStage;
+  const int tm = mt < kMaxMT ? 1 : p.tiles_m;
+  int s = 1;
+  while (p.tiles_n * tm * s * 2 <= 512 && stages / (2 * s) >= 4) s *= 2;
+  p.nsplit = s;
+  p.kslice = ((stages + s - 1) / s) * kStage;
+  p.nsplit = (K + p.kslice - 1) / p.kslice;
+  return p;
+}
+
+size_t gemm_partial_bytes(const GemmPlan& p, int M, int N) {
+  return p.nsplit > 1 ? (size_t)p.nsplit * M * N * sizeof(float) : 0;
+}
+
+bool gemm_supported(int K) { return K % kStage == 0; }
+
+template <int BITS, bool SF16, int MT, int GS>
+static hipError_t launch_mt(const QmvArgs& a, const GemmPlan& p, const u32x4* xh, const float* rsc,
+                            float* part) {
+  const int total = p.tiles_n * p.tiles_m * p.nsplit;
+  const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
+  hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS>), dim3(grid), dim3(64 * kWaves), 0, a.stream,
+                     xh, rsc, (const uint32_t*)a.w, (const uint16_t*)a.scales,
+                     (const uint16_t*)a.biases, part, a.out, a.odt, a.M, a.N, a.K, p.kslice,
+                     p.tiles_n, p.tiles_m, p.nsplit);
+  return hipGetLastError();
+}
+
+template <int BITS, bool SF16, int GS>
+static hipError_t launch_g(const QmvArgs& a, const GemmPlan& p, const u32x4* xh, const float* rsc,
+                           float* part) {
+  switch (p.mt) {
+    case 1: return launch_mt<BITS, SF16, 1, GS>(a, p, xh, rsc, part);
+    case 2: return launch_mt<BITS, SF16, 2, GS>(a, p, xh, rsc, part);
+    case 4: return launch_mt<BITS, SF16, 4, GS>(a, p, xh, rsc, part);
+    default: return launch_mt<BITS, SF16, 8, GS>(a, p, xh, rsc, part);
+  }
+}
+
+template <int BITS, bool SF16>
+static hipError_t launch_s(const QmvArgs& a, const GemmPlan& p, const u32x4* xh, const float* rsc,
+                           float* part) {
+  switch (a.gs) {
+    case 32: return launch_g<BITS, SF16, 32>(a, p, xh, rsc, part);
+    case 64: return launch_g<BITS, SF16, 64>(a, p, xh, rsc, part);
+    default: return launch_g<BITS, SF16, 128>(a, p, xh, rsc, part);
+  }
+}
+
+// `xh`/`rsc` as written by launch_prep_x; `part` holds gemm_partial_bytes.
+hipError_t launch_gemm(const QmvArgs& a, const GemmPlan& p, const void* xh, const float* rsc,
+                       float* part) {
+  hipError_t e;
+  const u32x4* x4 = static_cast<const u32x4*>(xh);
+  const bool sf16 = a.sdt == DT_F16;
+  if (a.bits == 4)
+    e = sf16 ? launch_s<4, true>(a, p, x4, rsc, part) : launch_s<4, false>(a, p, x4, rsc, part);
+  else
+    e = sf16 ? launch_s<8, true>(a, p, x4, rsc, part) : launch_s<8, false>(a, p, x4, rsc, part);
+  if (e != hipSuccess || p.nsplit == 1) return e;
+  const int64_t MN = (int64_t)a.M * a.N;
+  hipLaunchKernelGGL(gemm_reduce, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, a.stream, part,
+                     a.out, a.odt, MN, p.nsplit);
+  return hipGetLastError();
+}
+
+}  // namespace kh

@@ -45,6 +45,23 @@ hipError_t launch_fill_u32(void* p, int64_t n, uint32_t value, hipStream_t strea
 hipError_t launch_qmm(const QmvArgs& a, void* ws);
 size_t qmm_workspace_bytes(int M, int K);
 
+// x -> float16 rows scaled by an exact power of two (rsc[m] = 2^e_m), in the
+// pair order of the code operands: xh holds M*K*2 bytes, 16-byte aligned.
+hipError_t launch_prep_x(const QmvArgs& a, void* xh, float* rsc);
+
+// Quantized GEMM for every M above the VALU-GEMV range (K % 128 == 0): a
+// (16*mt) x 256 tile per workgroup, float16 MFMA on weights dequantised once
+// in registers, deterministic split-K. The plan depends on M only through mt.
+struct GemmPlan {
+  int mt, tiles_m, tiles_n, nsplit, kslice;
+};
+GemmPlan plan_gemm(int M, int N, int K, int bits);
+bool gemm_supported(int K);
+size_t gemm_partial_bytes(const GemmPlan& p, int M, int N);
+// xh/rsc from launch_prep_x; part: gemm_partial_bytes(p) bytes (unused if 0).
+hipError_t launch_gemm(const QmvArgs& a, const GemmPlan& p, const void* xh, const float* rsc,
+                       float* part);
+
 // Any dtype / alignment / transpose: one thread per output, fp32 fma chain.
 hipError_t launch_qmm_generic(const QmvArgs& a, bool transpose);
 

@@ -318,9 +318,8 @@ static hipError_t launch_gs(const QmvArgs& a, const u32x4* xh, const float* rsc)
 
 // `ws` holds qmm_workspace_bytes(M, K) bytes (16-byte aligned). Scales and
 // biases are float16 or bfloat16.
-hipError_t launch_qmm(const QmvArgs& a, void* ws) {
-  u32x4* xh = static_cast<u32x4*>(ws);
-  float* rsc = reinterpret_cast<float*>(static_cast<char*>(ws) + (size_t)a.M * a.K * 2);
+hipError_t launch_prep_x(const QmvArgs& a, void* xh_, float* rsc) {
+  u32x4* xh = static_cast<u32x4*>(xh_);
   const bool xbf16 = a.xdt == DT_BF16;
 #define KH_PREP(B, X) \
   hipLaunchKernelGGL((qmm_prep_x<B, X>), dim3(a.M), dim3(256), 0, a.stream, (const uint16_t*)a.x, xh, rsc, a.K)
@@ -330,7 +329,13 @@ hipError_t launch_qmm(const QmvArgs& a, void* ws) {
     if (xbf16) KH_PREP(8, true); else KH_PREP(8, false);
   }
 #undef KH_PREP
-  hipError_t e = hipGetLastError();
+  return hipGetLastError();
+}
+
+hipError_t launch_qmm(const QmvArgs& a, void* ws) {
+  u32x4* xh = static_cast<u32x4*>(ws);
+  float* rsc = reinterpret_cast<float*>(static_cast<char*>(ws) + (size_t)a.M * a.K * 2);
+  hipError_t e = launch_prep_x(a, xh, rsc);
   if (e != hipSuccess) return e;
   return a.bits == 4 ? launch_gs<4>(a, xh, rsc) : launch_gs<8>(a, xh, rsc);
 }

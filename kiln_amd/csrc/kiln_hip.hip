@@ -309,6 +309,18 @@ int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
     e = kh::launch_qmm_generic(a, transpose);
   } else if (M <= kh::gemv_max_m((int)K, bits) && kh::gemv_fits(M, N, K, bits, gs)) {
     e = kh::launch_gemv(a);
+  } else if (kh::gemm_supported((int)K)) {
+    // workspace: float16 activations | per-row scales | split-K partials
+    const kh::GemmPlan p = kh::plan_gemm((int)M, (int)N, (int)K, bits);
+    const size_t xb = (size_t)M * K * 2, rb = ((size_t)M * 4 + 255) / 256 * 256;
+    const size_t bytes = xb + rb + kh::gemm_partial_bytes(p, (int)M, (int)N);
+    Workspace ws;
+    if (!workspace(st, (bytes + 3) / 4, &ws, &rc, op)) return rc;
+    char* base = reinterpret_cast<char*>(ws.data);
+    float* rsc = reinterpret_cast<float*>(base + xb);
+    e = kh::launch_prep_x(a, base, rsc);
+    if (e == hipSuccess)
+      e = kh::launch_gemm(a, p, base, rsc, reinterpret_cast<float*>(base + xb + rb));
   } else if (M <= kh::kDecodeMaxM) {
     e = kh::launch_qmv(a);
   } else {

@@ -46,3 +46,24 @@ def gemv_max_m(K: int, bits: int) -> int:
     while -(-nch // (64 * I)) > 8:
         I += 1
     return 4 if I == 1 else 2 if I == 2 else 1 if I <= 4 else 0
+
+
+def decode_regime(M: int, K: int, bits: int):
+    """Which kernel (and tiling class) kh_quantized_matmul uses for a
+    transpose=true call with bf16/f16 x and 16-bit scales: rows of the result
+    are bitwise identical for every M of one regime."""
+    if M <= gemv_max_m(K, bits):
+        return ("gemv",)
+    if K % 128 == 0:
+        mt = 1
+        while mt < 8 and 16 * mt < M:
+            mt *= 2
+        return ("gemm", mt, -(-M // 128) if mt == 8 else 1)
+    return ("qmv",) if M <= 16 else ("qmm", -(-M // 256))
+
+
+def exact_weights(M: int, K: int, bits: int) -> bool:
+    """True where every dequantised weight enters the products unrounded
+    (the decode kernels); the GEMM kernels round each weight once to fp16."""
+    r = decode_regime(M, K, bits)[0]
+    return r in ("gemv", "qmv")

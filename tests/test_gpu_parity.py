@@ -16,7 +16,7 @@ import torch
 from kiln_amd import ops
 from kiln_amd.workloads import make_linear_numpy, make_x_numpy
 
-from _util import dev, gemv_max_m, host, parity_metrics
+from _util import decode_regime, dev, exact_weights, gemv_max_m, host, parity_metrics
 
 pytestmark = pytest.mark.gpu
 
@@ -50,13 +50,13 @@ def _run(L, x, gs, bits, xdt, sdt, odt, transpose=True):
 EXACT_REL, F16W_REL = 3e-5, 2.0 ** -11 + 3e-5
 
 
-def rel_for(M, transpose=True):
-    return EXACT_REL if (M <= 16 or not transpose) else F16W_REL
+def rel_for(M, K, bits, transpose=True):
+    return EXACT_REL if (not transpose or exact_weights(M, K, bits)) else F16W_REL
 
 
 def _check_f32(oracle, L, x, gs, bits, xdt, sdt, y, transpose=True, rel=None):
     if rel is None:
-        rel = rel_for(x.reshape(-1, x.shape[-1]).shape[0], transpose)
+        rel = rel_for(x.reshape(-1, x.shape[-1]).shape[0], x.shape[-1], bits, transpose)
     ref = oracle.quantized_matmul_f32(x, xdt, L["w"], L["scales"], L["biases"], sdt, gs, bits, transpose)
     W = oracle.to_f32(oracle.dequantize(L["w"], L["scales"], L["biases"], sdt, gs, bits, "f32"), "f32")
     mag = np.abs(oracle.to_f32(x, xdt)).astype(np.float64) @ np.abs(W.T if transpose else W).astype(np.float64)
@@ -125,25 +125,21 @@ def test_qmm_leading_dims_and_empty(oracle):
     assert tuple(e.shape) == (0, 32)
 
 
-@pytest.mark.parametrize("bits,gs,K", [(4, 64, 1024), (8, 128, 1024), (4, 32, 1024), (8, 64, 9216)])
+@pytest.mark.parametrize("bits,gs,K", [(4, 64, 1024), (8, 128, 1024), (4, 32, 1024), (8, 64, 9216),
+                                       (4, 32, 1056)])
 def test_rows_are_m_invariant(bits, gs, K):
     """Row r of the result is bitwise the same for every M served by the same
-    kernel: 1..gemv_max_m (VALU decode), ..16 (MFMA decode) and 17..N
-    (prefill) — the property Kiln's calibration probes
-    (crates/kiln-models/src/nn.rs:301-327)."""
+    kernel and tiling class (decode_regime) — the property Kiln's calibration
+    probes (crates/kiln-models/src/nn.rs:301-327)."""
     N = 272
     L, x = _case(200, N, K, gs, bits, seed=21)
-    g = gemv_max_m(K, bits)
-    run = lambda M: _run(L, x[:M], gs, bits, "bf16", "f16", "bf16")
-    small = run(g)
-    for M in range(1, g):
-        assert np.array_equal(run(M), small[:M]), M
-    dec = run(16)
-    for M in sorted({g + 1, 5, 15} - set(range(g + 1))):
-        assert np.array_equal(run(M), dec[:M]), M
-    pre = _run(L, x, gs, bits, "bf16", "f16", "bf16")
-    for M in (17, 33, 64, 129):
-        assert np.array_equal(run(M), pre[:M]), M
+    groups = {}
+    for M in (1, 2, 3, 4, 5, 6, 15, 16, 17, 20, 31, 32, 33, 64, 65, 100, 128, 129, 200):
+        groups.setdefault(decode_regime(M, K, bits), []).append(M)
+    for regime, Ms in groups.items():
+        big = _run(L, x[:max(Ms)], gs, bits, "bf16", "f16", "bf16")
+        for M in Ms[:-1]:
+            assert np.array_equal(_run(L, x[:M], gs, bits, "bf16", "f16", "bf16"), big[:M]), (regime, M)
 
 
 # Shapes that exercise every VALU-decode plan: I = 1..4 chunks per lane slot,
