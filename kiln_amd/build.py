@@ -56,6 +56,12 @@ def build(verbose: bool = False, out: str = LIB, extra=(), build_dir: str = BUIL
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    # A kernel template whose host-side stub was not emitted links into a
+    # shared library without complaint; refuse such a library here.
+    nm = subprocess.run(["nm", "-C", "--undefined-only", tmp], capture_output=True, text=True)
+    missing = [l for l in nm.stdout.splitlines() if "__device_stub__" in l]
+    if missing:
+        raise RuntimeError("kernel launch stubs missing from the library:\n" + "\n".join(missing[:10]))
     os.replace(tmp, out)
     if verbose:
         print(f"built {out}")
