@@ -1,4 +1,4 @@
-// kh_gemv.hip — decode quantized GEMV for gfx950 at M <= 4: one pass over
+// kh_gemv.hip — decode quantized GEMV for gfx950 at M <= 8: one pass over
 // the packed weights, every load issued up front, VALU dot products.
 //
 // Computes y[m, n] = sum_k x[m, k] * (s[n, g(k)] * q[n, k] + b[n, g(k)])
@@ -37,6 +37,9 @@ namespace kh {
 #define KH_GEMV_WAVES 2048  // waves per launch wanted before fewer rows per workgroup
 #endif
 
+#ifndef KH_GEMV_MAX_M
+#define KH_GEMV_MAX_M 8  // largest M served with one chunk per lane slot (4 or 8)
+#endif
 #ifndef KH_GEMV_RMAX
 #define KH_GEMV_RMAX 16  // rows per workgroup with one chunk per lane slot
 #endif
@@ -318,10 +321,17 @@ hipError_t launch_one(const QmvArgs& a, const GemvPlan& p) {
 template <int BITS, bool XBF16, bool SBF16, int M>
 hipError_t launch_m(const QmvArgs& a, const GemvPlan& p) {
   if (p.I == 1) {
-    if (p.R == 16) return launch_one<BITS, XBF16, SBF16, M, 16, 1>(a, p);
-    if (p.R == 8) return launch_one<BITS, XBF16, SBF16, M, 8, 1>(a, p);
-    if (p.R == 4) return launch_one<BITS, XBF16, SBF16, M, 4, 1>(a, p);
-    return launch_one<BITS, XBF16, SBF16, M, 2, 1>(a, p);
+    // At M = 8 the activations take 8x16 registers: at most 4 rows per
+    // workgroup. (R does not change any output's summation order.)
+    if constexpr (M == 8) {
+      if (p.R >= 4) return launch_one<BITS, XBF16, SBF16, 8, 4, 1>(a, p);
+      return launch_one<BITS, XBF16, SBF16, 8, 2, 1>(a, p);
+    } else {
+      if (p.R == 16) return launch_one<BITS, XBF16, SBF16, M, 16, 1>(a, p);
+      if (p.R == 8) return launch_one<BITS, XBF16, SBF16, M, 8, 1>(a, p);
+      if (p.R == 4) return launch_one<BITS, XBF16, SBF16, M, 4, 1>(a, p);
+      return launch_one<BITS, XBF16, SBF16, M, 2, 1>(a, p);
+    }
   }
   if constexpr (M <= 2) {
     if (p.I == 2) {
@@ -340,7 +350,8 @@ template <int BITS, bool XBF16, bool SBF16>
 hipError_t launch_s(const QmvArgs& a, const GemvPlan& p) {
   if (a.M == 1) return launch_m<BITS, XBF16, SBF16, 1>(a, p);
   if (a.M == 2) return launch_m<BITS, XBF16, SBF16, 2>(a, p);
-  return launch_m<BITS, XBF16, SBF16, 4>(a, p);
+  if (a.M <= 4) return launch_m<BITS, XBF16, SBF16, 4>(a, p);
+  return launch_m<BITS, XBF16, SBF16, 8>(a, p);
 }
 
 template <int BITS, bool XBF16>
@@ -357,7 +368,7 @@ bool gemv_fits(int64_t M, int64_t N, int64_t K, int bits, int gs) {
 
 int gemv_max_m(int K, int bits) {
   const int I = plan_gemv(1, K, bits).I;
-  return I == 1 ? 4 : (I == 2 ? 2 : (I <= 4 ? 1 : 0));
+  return I == 1 ? KH_GEMV_MAX_M : (I == 2 ? 2 : (I <= 4 ? 1 : 0));
 }
 
 hipError_t launch_gemv(const QmvArgs& a) {

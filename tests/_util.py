@@ -45,7 +45,7 @@ def gemv_max_m(K: int, bits: int) -> int:
     I = 1
     while -(-nch // (64 * I)) > 8:
         I += 1
-    return 4 if I == 1 else 2 if I == 2 else 1 if I <= 4 else 0
+    return 8 if I == 1 else 2 if I == 2 else 1 if I <= 4 else 0
 
 
 def decode_regime(M: int, K: int, bits: int):
