@@ -136,6 +136,8 @@ def main():
     dom_bytes = call_bytes(dN, dK, 1, bits, gs)
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
 
+    fused = fused_step(torch, ops, layers, shapes, graph_us, dev, g, gs, bits, copies, reps)
+
     sweep = {} if args.no_sweep else run_sweep(torch, ops, layers, shapes, graph_us, layer_fns,
                                                layer_copies, make_linear_device, dev, g)
 
@@ -166,11 +168,41 @@ def main():
         "per_shape_us": {k: round(v, 2) for k, v in per_shape_us.items()},
         "per_shape_gbs": {n: round(call_bytes(N, K, 1, bits, gs) / (per_shape_us[n] * 1e-6) / 1e9, 1)
                           for n, N, K in shapes},
+        "fused_step": fused,
         "prefill_m2048_tflops": sweep.get("llama-3-8b", {}).get("prefill", {}).get("2048", {}).get("tflops"),
         "sweep": sweep,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def fused_step(torch, ops, layers, shapes, graph_us, dev, g, gs, bits, copies, reps):
+    """The same M = 1 layer through the fused entry points (SURVEY next row:
+    fused neighbours): q|k|v in one kh_quantized_matmul_multi launch, o,
+    silu(gate)*up in one kh_quantized_gate_up launch, down. Algorithmic bytes
+    count x once per launch and the one activation output."""
+    Ns = {n: (N, K) for n, N, K in shapes}
+    x = torch.randn((1, Ns["q"][1]), generator=g, device=dev).bfloat16()
+    xd = torch.randn((1, Ns["down"][1]), generator=g, device=dev).bfloat16()
+    qkv = [torch.empty((1, Ns[n][0]), dtype=torch.bfloat16, device=dev) for n in ("q", "k", "v")]
+    o = torch.empty((1, Ns["o"][0]), dtype=torch.bfloat16, device=dev)
+    act = torch.empty((1, Ns["gate"][0]), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((1, Ns["down"][0]), dtype=torch.bfloat16, device=dev)
+
+    def step(c):
+        L = layers[c]
+        W = lambda n: (L[n]["w"], L[n]["scales"], L[n]["biases"])
+        ops.quantized_matmul_multi(x, [W("q"), W("k"), W("v")], True, gs, bits, outs=qkv)
+        ops.quantized_matmul(x, *W("o"), True, gs, bits, out=o)
+        ops.quantized_gate_up(x, W("gate"), W("up"), gs, bits, out=act)
+        ops.quantized_matmul(xd, *W("down"), True, gs, bits, out=y)
+
+    us = graph_us(step, copies, reps)
+    wb = lambda n: Ns[n][0] * Ns[n][1] * bits // 8 + 2 * Ns[n][0] * (Ns[n][1] // gs) * 2
+    nbytes = (sum(wb(n) for n in ("q", "k", "v", "o", "gate", "up", "down")) + 2 * 2 * Ns["q"][1]
+              + 2 * Ns["down"][1] + 2 * (sum(Ns[n][0] for n in ("q", "k", "v", "o", "down")) + Ns["gate"][0]))
+    return {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "launches": 4,
+            "bytes": nbytes}
 
 
 def run_sweep(torch, ops, l8_layers, l8_shapes, graph_us, layer_fns, layer_copies, make_linear_device,

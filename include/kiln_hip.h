@@ -15,6 +15,8 @@
  *   kh_add                  replaces mlx_add for the bias add of Linear::forward
  *                           (nn.rs:98-100, ops::add): res = a + b, b broadcast
  *                           over a's leading dimensions.
+ *   kh_quantized_matmul_multi  the q/k/v projections (nn.rs:724-726) on one x.
+ *   kh_quantized_gate_up    silu(gate(x)) * up(x) of the gated MLP (nn.rs:284-294).
  *   kh_quantized_embedding  the fused form of Embedding::lookup
  *                           (nn.rs:159-176): three take(axis=0) calls
  *                           followed by dequantize, in one pass.
@@ -131,6 +133,31 @@ int kh_dequantize(kh_array* res, const kh_array* w, const kh_array* scales,
  * [-V, V) yields a zero row (HBM is never read out of bounds). */
 int kh_take(kh_array* res, const kh_array* a, const kh_array* indices,
             kh_stream stream);
+
+/* Several quantized_matmul calls that share x: res[i] = x @ dequantize(w[i])^T
+ * (transpose=true) for i < n, each exactly as kh_quantized_matmul computes it.
+ * Replaces the q/k/v projection triple of the attention block
+ * (crates/kiln-models/src/nn.rs:724-726: three Linear::forward on one x);
+ * with transpose=true, 16-bit x and scales and M within the decode GEMV's
+ * range, up to 4 parts run in one launch. */
+int kh_quantized_matmul_multi(int n, kh_array* const* res, const kh_array* x,
+                              const kh_array* const* w, const kh_array* const* scales,
+                              const kh_array* const* biases, bool transpose,
+                              kh_optional_int group_size, kh_optional_int bits,
+                              const char* mode, kh_stream stream);
+
+/* res = silu(x @ gate^T) * (x @ up^T): the input of the gated MLP's down
+ * projection (crates/kiln-models/src/nn.rs:284-294, Activation::Silu), which
+ * the reference forms with two quantized_matmul calls, sigmoid and two
+ * multiplies. Every intermediate is rounded to res's dtype as those arrays
+ * are: gate and up; sigmoid(gate), evaluated in float32; gate*sigmoid; and
+ * the final product. Shapes as kh_quantized_matmul with transpose=true; gate
+ * and up have equal shapes. One launch where the decode GEMV applies. */
+int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gate,
+                         const kh_array* scales_gate, const kh_array* biases_gate,
+                         const kh_array* w_up, const kh_array* scales_up,
+                         const kh_array* biases_up, kh_optional_int group_size,
+                         kh_optional_int bits, const char* mode, kh_stream stream);
 
 /* res = dequantize(take(w, ids), take(scales, ids), take(biases, ids)):
  * the quantized embedding lookup. ids uint32|int32 of any shape; w [V, H*bits/32];

@@ -21,8 +21,9 @@ STATUS = {0: "KH_OK", 1: "KH_ERR_INVALID_ARGUMENT", 2: "KH_ERR_UNSUPPORTED",
           3: "KH_ERR_DEVICE", 4: "KH_ERR_NO_DEVICE"}
 
 # Every symbol include/kiln_hip.h declares.
-EXPORTS = ("kh_quantized_matmul", "kh_dequantize", "kh_take", "kh_quantized_embedding",
-           "kh_add", "kh_last_error", "kh_version")
+EXPORTS = ("kh_quantized_matmul", "kh_quantized_matmul_multi", "kh_quantized_gate_up",
+           "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add", "kh_last_error",
+           "kh_version")
 
 
 class KhArray(ctypes.Structure):
@@ -55,14 +56,20 @@ def lib() -> ctypes.CDLL:
         P = ctypes.POINTER(KhArray)
         L.kh_quantized_matmul.argtypes = [P, P, P, P, P, ctypes.c_bool, KhOptionalInt,
                                           KhOptionalInt, ctypes.c_char_p, ctypes.c_void_p]
+        PP = ctypes.POINTER(P)
+        L.kh_quantized_matmul_multi.argtypes = [ctypes.c_int, PP, P, PP, PP, PP, ctypes.c_bool,
+                                                KhOptionalInt, KhOptionalInt, ctypes.c_char_p,
+                                                ctypes.c_void_p]
+        L.kh_quantized_gate_up.argtypes = [P, P, P, P, P, P, P, P, KhOptionalInt, KhOptionalInt,
+                                           ctypes.c_char_p, ctypes.c_void_p]
         L.kh_dequantize.argtypes = [P, P, P, P, KhOptionalInt, KhOptionalInt, ctypes.c_char_p,
                                     ctypes.c_void_p]
         L.kh_take.argtypes = [P, P, P, ctypes.c_void_p]
         L.kh_add.argtypes = [P, P, P, ctypes.c_void_p]
         L.kh_quantized_embedding.argtypes = [P, P, P, P, P, KhOptionalInt, KhOptionalInt,
                                              ctypes.c_char_p, ctypes.c_void_p]
-        for f in ("kh_quantized_matmul", "kh_dequantize", "kh_take", "kh_quantized_embedding",
-                  "kh_add"):
+        for f in ("kh_quantized_matmul", "kh_quantized_matmul_multi", "kh_quantized_gate_up",
+                  "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add"):
             getattr(L, f).restype = ctypes.c_int
         L.kh_last_error.restype = ctypes.c_char_p
         L.kh_version.restype = ctypes.c_char_p

@@ -54,6 +54,26 @@ __device__ __forceinline__ void store_from_f32(void* p, int dt, int64_t i, float
   }
 }
 
+// v rounded to dtype dt (round-to-nearest-even) and read back as float32.
+__device__ __forceinline__ float round_to(float v, int dt) {
+  if (dt == DT_F32) return v;
+  return dt == DT_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(v)) : f16_bits_to_f32(f32_to_f16_bits(v));
+}
+
+// The gated-MLP activation of Kiln's llama/qwen MLP (crates/kiln-models/src/
+// nn.rs:284-294): silu(gate) * up = gate * sigmoid(gate) * up, with every
+// intermediate an array of the output dtype dt as in the reference's op
+// graph: gate and up rounded to dt, sigmoid evaluated in float32 from the
+// rounded gate and rounded, gate*sigmoid rounded, and the final product
+// returned in float32 for the caller's single rounding store.
+__device__ __forceinline__ float silu_mul(float g, float u, int dt) {
+  g = round_to(g, dt);
+  u = round_to(u, dt);
+  const float sg = round_to(1.f / (1.f + expf(-g)), dt);
+  const float a = round_to(g * sg, dt);
+  return a * u;
+}
+
 // Round a pair to dt and pack the two 16-bit results (lo = a).
 __device__ __forceinline__ uint32_t pack2(float a, float b, int dt) {
   uint32_t ha = dt == DT_BF16 ? f32_to_bf16_bits(a) : f32_to_f16_bits(a);

@@ -157,6 +157,13 @@ __global__ void add_kernel(const void* __restrict__ a, int adt, const void* __re
   store_from_f32(res, rdt, i, load_as_f32(a, adt, i) + load_as_f32(b, bdt, i % nb));
 }
 
+__global__ void silu_mul_kernel(const void* __restrict__ g, const void* __restrict__ u,
+                                void* __restrict__ res, int dt, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  store_from_f32(res, dt, i, silu_mul(load_as_f32(g, dt, i), load_as_f32(u, dt, i), dt));
+}
+
 __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -249,6 +256,14 @@ hipError_t launch_qmm_generic(const QmvArgs& a, bool transpose) {
   else
     hipLaunchKernelGGL(qmm_generic_kernel<8>, grid, block, 0, a.stream, a.x, a.xdt, wp, a.scales,
                        a.biases, a.sdt, a.out, a.odt, a.M, a.N, a.K, a.gs, transpose ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const void* g, const void* u, void* res, int dt, int64_t n,
+                           hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, g, u, res,
+                     dt, n);
   return hipGetLastError();
 }
 

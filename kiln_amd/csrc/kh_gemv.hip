@@ -53,6 +53,7 @@ namespace kh {
 namespace {
 
 constexpr int kGemvMaxWaves = 8;
+constexpr int kGemvMaxParts = 4;
 
 // Raw buffer loads: a descriptor per tensor (uniform, in SGPRs), the row
 // offset as the scalar offset and a 32-bit lane offset, so no per-lane 64-bit
@@ -149,11 +150,25 @@ __device__ __forceinline__ void butterfly(float* acc, int lane) {
   }
 }
 
-template <int BITS, bool XBF16, bool SBF16, int M, int R, int I>
+// Weight sets of one launch: parts share x (and K, bits, group size, dtypes);
+// part i owns workgroups [wg0, next part's wg0). With GU the launch has two
+// parts of equal N (gate, up) and every workgroup owns the same rows of both.
+struct GemvParts {
+  const uint32_t* w[kGemvMaxParts];
+  const uint16_t* scales[kGemvMaxParts];
+  const uint16_t* biases[kGemvMaxParts];
+  void* out[kGemvMaxParts];
+  int N[kGemvMaxParts];
+  int wg0[kGemvMaxParts];
+  int nparts;
+};
+
+// RT rows per workgroup: R rows of one part, or (GU) R = RT/2 rows of the
+// gate and the same R rows of the up projection, stored as silu(gate)*up.
+template <int BITS, bool XBF16, bool SBF16, int M, int RT, int I, bool GU>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
-    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    void* __restrict__ out, int odt, int Mrows, int N, int K, int cshift) {
+    const uint16_t* __restrict__ x, const GemvParts parts, int odt, int Mrows, int K, int cshift) {
+  constexpr int R = RT;
   constexpr int CPC = 128 / BITS;  // codes per chunk
   constexpr int NP = CPC / 2;      // operand pairs per chunk
   constexpr int NXV = CPC / 8;     // 16-byte activation loads per chunk
@@ -169,7 +184,12 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
   const int nch = K / CPC;           // chunks per row
   const int wpr = nch * 4;           // words per row
   const int G = nch >> cshift;       // groups per row (cshift = log2(group_size / CPC))
-  const int row0 = blockIdx.x * R;
+  constexpr int RP = GU ? R / 2 : R;  // rows per part of this workgroup
+  int part = 0;                       // (GU: the gate's part; up is part 1)
+  if (!GU)
+    for (int i = 1; i < parts.nparts; ++i) part = (int)blockIdx.x >= parts.wg0[i] ? i : part;
+  const int N = parts.N[part];
+  const int row0 = ((int)blockIdx.x - parts.wg0[part]) * RP;
 
   int cidx[I];
   bool live[I];
@@ -183,8 +203,15 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
   // ---- issue every load: activations, codes, scale/bias halves. Each
   // address is a row base (uniform across the wave) plus a 32-bit lane
   // offset, the form the scalar-base global loads take.
-  const __amdgpu_buffer_rsrc_t bx = buffer_of(x), bw = buffer_of(w);
-  const __amdgpu_buffer_rsrc_t bs = buffer_of(scales), bb = buffer_of(biases);
+  const __amdgpu_buffer_rsrc_t bx = buffer_of(x);
+  // descriptors of the part (GU: [0] gate, [1] up)
+  __amdgpu_buffer_rsrc_t bw[2], bs[2], bb[2];
+#pragma unroll
+  for (int h = 0; h < (GU ? 2 : 1); ++h) {
+    bw[h] = buffer_of(parts.w[part + h]);
+    bs[h] = buffer_of(parts.scales[part + h]);
+    bb[h] = buffer_of(parts.biases[part + h]);
+  }
   u32x4 xr[I][M][NXV];
 #pragma unroll
   for (int i = 0; i < I; ++i)
@@ -202,11 +229,12 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
   uint32_t sr[R][I], br[R][I];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int n = row0 + r < N ? row0 + r : N - 1;
+    const int h = GU && r >= RP ? 1 : 0;  // compile-time once unrolled
+    const int n = row0 + r % RP < N ? row0 + r % RP : N - 1;
 #pragma unroll
     for (int i = 0; i < I; ++i) {
       const u32x4 v = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(bw, cidx[i] * 16, n * wpr * 4, kCodeAux));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(bw[h], cidx[i] * 16, n * wpr * 4, kCodeAux));
       q[r][i][0] = v[0];
       q[r][i][1] = v[1];
       q[r][i][2] = v[2];
@@ -216,8 +244,8 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
         sr[r][i] = 0x3c00u + r;
         br[r][i] = 0x3c00u + go;
       } else {
-        sr[r][i] = __builtin_amdgcn_raw_buffer_load_b16(bs, go, n * G * 2, 0);
-        br[r][i] = __builtin_amdgcn_raw_buffer_load_b16(bb, go, n * G * 2, 0);
+        sr[r][i] = __builtin_amdgcn_raw_buffer_load_b16(bs[h], go, n * G * 2, 0);
+        br[r][i] = __builtin_amdgcn_raw_buffer_load_b16(bb[h], go, n * G * 2, 0);
       }
     }
   }
@@ -283,13 +311,23 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
   constexpr int LNV = __builtin_ctz(NV);
   if ((lane & ((64 >> LNV) - 1)) == 0) red[wave][lane >> (6 - LNV)] = acc[0];
   __syncthreads();
-  if (tid < NV) {
-    const int W = nth >> 6;
+  const int W = nth >> 6;
+  if (!GU && tid < NV) {
     float s = red[0][tid];
     for (int v = 1; v < W; ++v) s += red[v][tid];
     const int r = tid / M, m = tid % M;
     const int n = row0 + r;
-    if (n < N && m < Mrows) store_from_f32(out, odt, (int64_t)m * N + n, s);
+    if (n < N && m < Mrows) store_from_f32(parts.out[part], odt, (int64_t)m * N + n, s);
+  }
+  if (GU && tid < NV / 2) {  // partial j = r*M + m: gate rows first, then up rows
+    float g = red[0][tid], u = red[0][tid + NV / 2];
+    for (int v = 1; v < W; ++v) {
+      g += red[v][tid];
+      u += red[v][tid + NV / 2];
+    }
+    const int r = tid / M, m = tid % M;
+    const int n = row0 + r;
+    if (n < N && m < Mrows) store_from_f32(parts.out[0], odt, (int64_t)m * N + n, silu_mul(g, u, odt));
   }
 }
 
@@ -307,19 +345,35 @@ GemvPlan plan_gemv(int N, int K, int bits) {
   return {waves, I, R};
 }
 
+struct GemvLaunch {
+  const QmvArgs* a;  // shared fields (x, dtypes, M, K, gs, bits, stream) from a[0]
+  GemvParts parts;
+  int total_wgs;
+  bool gu;
+};
+
 template <int BITS, bool XBF16, bool SBF16, int M, int R, int I>
-hipError_t launch_one(const QmvArgs& a, const GemvPlan& p) {
+hipError_t launch_one(const GemvLaunch& L, const GemvPlan& p) {
   constexpr int CPC = 128 / BITS;
+  const QmvArgs& a = *L.a;
   const int cshift = __builtin_ctz(a.gs / CPC);
-  hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, R, I>), dim3((a.N + R - 1) / R),
-                     dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, (const uint32_t*)a.w,
-                     (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.out, a.odt, a.M, a.N,
-                     a.K, cshift);
+  if (L.gu) {
+    if constexpr (2 * R * M <= 64)
+      hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, 2 * R, I, true>), dim3(L.total_wgs),
+                         dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, L.parts, a.odt, a.M,
+                         a.K, cshift);
+    else
+      return hipErrorInvalidValue;
+  } else {
+    hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, R, I, false>), dim3(L.total_wgs),
+                       dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, L.parts, a.odt, a.M, a.K,
+                       cshift);
+  }
   return hipGetLastError();
 }
 
 template <int BITS, bool XBF16, bool SBF16, int M>
-hipError_t launch_m(const QmvArgs& a, const GemvPlan& p) {
+hipError_t launch_m(const GemvLaunch& a, const GemvPlan& p) {
   if (p.I == 1) {
     // At M = 8 the activations take 8x16 registers: at most 4 rows per
     // workgroup. (R does not change any output's summation order.)
@@ -347,16 +401,50 @@ hipError_t launch_m(const QmvArgs& a, const GemvPlan& p) {
 }
 
 template <int BITS, bool XBF16, bool SBF16>
-hipError_t launch_s(const QmvArgs& a, const GemvPlan& p) {
-  if (a.M == 1) return launch_m<BITS, XBF16, SBF16, 1>(a, p);
-  if (a.M == 2) return launch_m<BITS, XBF16, SBF16, 2>(a, p);
-  if (a.M <= 4) return launch_m<BITS, XBF16, SBF16, 4>(a, p);
-  return launch_m<BITS, XBF16, SBF16, 8>(a, p);
+hipError_t launch_s(const GemvLaunch& L, const GemvPlan& p) {
+  const int M = L.a->M;
+  if (M == 1) return launch_m<BITS, XBF16, SBF16, 1>(L, p);
+  if (M == 2) return launch_m<BITS, XBF16, SBF16, 2>(L, p);
+  if (M <= 4) return launch_m<BITS, XBF16, SBF16, 4>(L, p);
+  return launch_m<BITS, XBF16, SBF16, 8>(L, p);
 }
 
 template <int BITS, bool XBF16>
-hipError_t launch_x(const QmvArgs& a, const GemvPlan& p) {
-  return a.sdt == DT_BF16 ? launch_s<BITS, XBF16, true>(a, p) : launch_s<BITS, XBF16, false>(a, p);
+hipError_t launch_x(const GemvLaunch& L, const GemvPlan& p) {
+  return L.a->sdt == DT_BF16 ? launch_s<BITS, XBF16, true>(L, p) : launch_s<BITS, XBF16, false>(L, p);
+}
+
+// Rows per workgroup actually launched (the instantiation launch_m picks).
+int rows_launched(const GemvPlan& p, int M) {
+  if (p.I == 1 && M > 4) return p.R >= 4 ? 4 : 2;
+  return p.R;
+}
+
+hipError_t launch(GemvLaunch& L) {
+  const QmvArgs& a = *L.a;
+  int ntot = 0;
+  for (int i = 0; i < L.parts.nparts; ++i) ntot += L.parts.N[i];
+  GemvPlan p = plan_gemv(L.gu ? L.parts.N[0] : ntot, a.K, a.bits);
+  if (L.gu)  // the gate and up rows of a workgroup share its partial-sum lanes
+    while (p.R > 2 && 2 * rows_launched(p, a.M) * (a.M <= 2 ? a.M : (a.M <= 4 ? 4 : 8)) > 64) p.R >>= 1;
+  const int R = rows_launched(p, a.M);
+  L.total_wgs = 0;
+  for (int i = 0; i < L.parts.nparts; ++i) {
+    L.parts.wg0[i] = L.total_wgs;
+    if (!L.gu || i == 0) L.total_wgs += (L.parts.N[i] + R - 1) / R;
+  }
+  if (L.gu) L.parts.wg0[1] = 0;
+  const bool xbf16 = a.xdt == DT_BF16;
+  if (a.bits == 4) return xbf16 ? launch_x<4, true>(L, p) : launch_x<4, false>(L, p);
+  return xbf16 ? launch_x<8, true>(L, p) : launch_x<8, false>(L, p);
+}
+
+void set_part(GemvParts& P, int i, const QmvArgs& a) {
+  P.w[i] = (const uint32_t*)a.w;
+  P.scales[i] = (const uint16_t*)a.scales;
+  P.biases[i] = (const uint16_t*)a.biases;
+  P.out[i] = a.out;
+  P.N[i] = a.N;
 }
 
 }  // namespace
@@ -373,10 +461,28 @@ int gemv_max_m(int K, int bits) {
 
 hipError_t launch_gemv(const QmvArgs& a) {
   if (a.M < 1 || a.M > gemv_max_m(a.K, a.bits)) return hipErrorInvalidValue;
-  const GemvPlan p = plan_gemv(a.N, a.K, a.bits);
-  const bool xbf16 = a.xdt == DT_BF16;
-  if (a.bits == 4) return xbf16 ? launch_x<4, true>(a, p) : launch_x<4, false>(a, p);
-  return xbf16 ? launch_x<8, true>(a, p) : launch_x<8, false>(a, p);
+  GemvLaunch L{&a, {}, 0, false};
+  L.parts.nparts = 1;
+  set_part(L.parts, 0, a);
+  return launch(L);
+}
+
+hipError_t launch_gemv_multi(const QmvArgs* a, int n) {
+  if (n < 1 || n > kGemvMaxParts || a[0].M < 1 || a[0].M > gemv_max_m(a[0].K, a[0].bits))
+    return hipErrorInvalidValue;
+  GemvLaunch L{&a[0], {}, 0, false};
+  L.parts.nparts = n;
+  for (int i = 0; i < n; ++i) set_part(L.parts, i, a[i]);
+  return launch(L);
+}
+
+hipError_t launch_gemv_gate_up(const QmvArgs& gate, const QmvArgs& up) {
+  if (gate.M < 1 || gate.M > gemv_max_m(gate.K, gate.bits) || gate.N != up.N) return hipErrorInvalidValue;
+  GemvLaunch L{&gate, {}, 0, true};
+  L.parts.nparts = 2;
+  set_part(L.parts, 0, gate);
+  set_part(L.parts, 1, up);
+  return launch(L);
 }
 
 }  // namespace kh

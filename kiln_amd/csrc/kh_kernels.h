@@ -31,6 +31,12 @@ int gemv_max_m(int K, int bits);
 // The kernel addresses each operand with 32-bit byte offsets.
 bool gemv_fits(int64_t M, int64_t N, int64_t K, int bits, int gs);
 hipError_t launch_gemv(const QmvArgs& a);
+// Up to 4 weight sets sharing x (and M, K, bits, group size, dtypes), one
+// launch: q/k/v projections.
+hipError_t launch_gemv_multi(const QmvArgs* a, int n);
+// gate.out = silu(x gate^T) * (x up^T) (silu_mul sequence), one launch;
+// gate.N == up.N.
+hipError_t launch_gemv_gate_up(const QmvArgs& gate, const QmvArgs& up);
 
 // Decode path (M <= kDecodeMaxM; correct up to M = 64), MFMA on unscaled
 // codes with per-group fp32 scaling.
@@ -74,6 +80,10 @@ hipError_t launch_dequantize(const void* w, const void* scales, const void* bias
 hipError_t launch_embedding(const void* ids, bool ids_signed, int64_t T, const void* w,
                             const void* scales, const void* biases, int sdt, void* out, int odt,
                             int64_t V, int64_t H, int gs, int bits, hipStream_t stream);
+
+// res[i] = silu_mul(g[i], u[i]) in dtype dt (g, u, res all of dtype dt).
+hipError_t launch_silu_mul(const void* g, const void* u, void* res, int dt, int64_t n,
+                           hipStream_t stream);
 
 // res[i] = a[i] + b[i % nb] (float32 sum, rounded once to rdt).
 hipError_t launch_add(const void* a, int adt, const void* b, int bdt, void* res, int rdt, int64_t n,

@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <tuple>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -209,13 +210,17 @@ struct Workspace {
   float* data;
 };
 
-bool workspace(hipStream_t stream, size_t floats, Workspace* ws, int* rc, const char* op) {
+// `which` selects one of several independent buffers of the stream (0: the
+// kernels' own scratch; 1: intermediates of a composite call whose steps use
+// buffer 0).
+bool workspace(hipStream_t stream, size_t floats, Workspace* ws, int* rc, const char* op,
+               int which = 0) {
   static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> pool;
+  static std::map<std::tuple<int, hipStream_t, int>, std::pair<void*, size_t>> pool;
   int dev = 0;
   (void)hipGetDevice(&dev);
   std::lock_guard<std::mutex> lock(mu);
-  auto& slot = pool[{dev, stream}];
+  auto& slot = pool[{dev, stream, which}];
   const size_t bytes = kCounterBytes + floats * sizeof(float);
   if (slot.second < bytes) {
     // Under stream capture (e.g. a HIP graph being recorded) the stream may
@@ -265,11 +270,15 @@ const char* kh_last_error(void) { return g_last_error.c_str(); }
 
 const char* kh_version(void) { return "kiln-hip 0.1.0 (gfx950)"; }
 
-int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
-                        const kh_array* scales, const kh_array* biases, bool transpose,
-                        kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,
-                        kh_stream stream) {
-  const char* op = "quantized_matmul";
+namespace {
+
+// Validation of one quantized_matmul call (ops.rs:359-388 argument rules);
+// on success *a describes the call, *empty says there is nothing to compute.
+// The device check is the caller's, after every part has been validated.
+int prepare_qmm(const char* op, kh_array* res, const kh_array* x, const kh_array* w,
+                const kh_array* scales, const kh_array* biases, bool transpose,
+                kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,
+                kh_stream stream, kh::QmvArgs* a, bool* empty) {
   int gs, bits, rc;
   if ((rc = check_quant(op, group_size, bits_opt, mode, &gs, &bits))) return rc;
   if ((rc = check_array(x, op, "x"))) return rc;
@@ -295,23 +304,38 @@ int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
   const int64_t M = K ? numel(x) / K : numel(res) / (N ? N : 1);
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
     return fail(KH_ERR_UNSUPPORTED, "[%s] dimensions beyond 2^31 are not supported", op);
-  if (M == 0 || N == 0) return KH_OK;
-  if ((rc = check_device(op))) return rc;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  kh::QmvArgs a{x->data, x->dtype, w->data, scales->data, biases->data, scales->dtype, res->data,
-                res->dtype, (int)M, (int)N, (int)K, gs, bits, st};
+  *empty = M == 0 || N == 0;
+  if (*empty) return KH_OK;
+  *a = kh::QmvArgs{x->data, x->dtype, w->data, scales->data, biases->data, scales->dtype, res->data,
+                   res->dtype, (int)M, (int)N, (int)K, gs, bits, static_cast<hipStream_t>(stream)};
+  return KH_OK;
+}
+
+// The fast kernels take transpose=true, 16-bit x and scales, 16-byte aligned x and w.
+bool fast_path(const kh::QmvArgs& a, bool transpose) {
+  return a.K > 0 && transpose && a.xdt != KH_FLOAT32 && a.sdt != KH_FLOAT32 && aligned16(a.x) &&
+         aligned16(a.w);
+}
+
+bool gemv_path(const kh::QmvArgs& a) {
+  return a.M <= kh::gemv_max_m(a.K, a.bits) && kh::gemv_fits(a.M, a.N, a.K, a.bits, a.gs);
+}
+
+// Kernel dispatch of one validated call.
+int run_qmm(const char* op, const kh::QmvArgs& a, bool transpose) {
+  int rc;
+  hipError_t e;
+  const hipStream_t st = a.stream;
+  const int64_t M = a.M, N = a.N, K = a.K;
   // K == 0 takes the general kernel too: its empty sums write zeros (a
   // kernel, not a memset, so the call stays safe under graph capture).
-  const bool fast = K > 0 && transpose && x->dtype != KH_FLOAT32 && scales->dtype != KH_FLOAT32 &&
-                    aligned16(x->data) && aligned16(w->data);
-  hipError_t e;
-  if (!fast) {
+  if (!fast_path(a, transpose)) {
     e = kh::launch_qmm_generic(a, transpose);
-  } else if (M <= kh::gemv_max_m((int)K, bits) && kh::gemv_fits(M, N, K, bits, gs)) {
+  } else if (gemv_path(a)) {
     e = kh::launch_gemv(a);
   } else if (kh::gemm_supported((int)K)) {
     // workspace: float16 activations | per-row scales | split-K partials
-    const kh::GemmPlan p = kh::plan_gemm((int)M, (int)N, (int)K, bits);
+    const kh::GemmPlan p = kh::plan_gemm((int)M, (int)N, (int)K, a.bits);
     const size_t xb = (size_t)M * K * 2, rb = ((size_t)M * 4 + 255) / 256 * 256;
     const size_t bytes = xb + rb + kh::gemm_partial_bytes(p, (int)M, (int)N);
     Workspace ws;
@@ -329,6 +353,97 @@ int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
     if (!workspace(st, (bytes + 3) / 4, &ws, &rc, op)) return rc;
     e = kh::launch_qmm(a, ws.data);
   }
+  return e == hipSuccess ? KH_OK : hip_fail(op, e);
+}
+
+}  // namespace
+
+int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
+                        const kh_array* scales, const kh_array* biases, bool transpose,
+                        kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,
+                        kh_stream stream) {
+  const char* op = "quantized_matmul";
+  kh::QmvArgs a;
+  bool empty = false;
+  int rc = prepare_qmm(op, res, x, w, scales, biases, transpose, group_size, bits_opt, mode, stream, &a,
+                       &empty);
+  if (rc || empty) return rc;
+  if ((rc = check_device(op))) return rc;
+  return run_qmm(op, a, transpose);
+}
+
+int kh_quantized_matmul_multi(int n, kh_array* const* res, const kh_array* x,
+                              const kh_array* const* w, const kh_array* const* scales,
+                              const kh_array* const* biases, bool transpose,
+                              kh_optional_int group_size, kh_optional_int bits, const char* mode,
+                              kh_stream stream) {
+  const char* op = "quantized_matmul_multi";
+  if (n < 1 || !res || !w || !scales || !biases)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] n must be >= 1 with non-null part arrays (n=%d)", op, n);
+  std::vector<kh::QmvArgs> a(n);
+  bool any_empty = false;
+  for (int i = 0; i < n; ++i) {
+    bool empty = false;
+    const int rc = prepare_qmm(op, res[i], x, w[i], scales[i], biases[i], transpose, group_size, bits, mode,
+                               stream, &a[i], &empty);
+    if (rc) return rc;
+    any_empty |= empty;
+  }
+  if (int rc = check_device(op)) return rc;
+  if (any_empty) {  // some part has N == 0 (or M == 0): run the others one by one
+    for (int i = 0; i < n; ++i) {
+      int rc = kh_quantized_matmul(res[i], x, w[i], scales[i], biases[i], transpose, group_size, bits,
+                                   mode, stream);
+      if (rc) return rc;
+    }
+    return KH_OK;
+  }
+  bool fused = n <= 4;
+  for (int i = 0; i < n && fused; ++i)
+    fused = fast_path(a[i], transpose) && gemv_path(a[i]) && a[i].sdt == a[0].sdt && a[i].odt == a[0].odt;
+  if (fused) {
+    const hipError_t e = kh::launch_gemv_multi(a.data(), n);
+    return e == hipSuccess ? KH_OK : hip_fail(op, e);
+  }
+  for (int i = 0; i < n; ++i) {
+    const int rc = run_qmm(op, a[i], transpose);
+    if (rc) return rc;
+  }
+  return KH_OK;
+}
+
+int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gate,
+                         const kh_array* scales_gate, const kh_array* biases_gate,
+                         const kh_array* w_up, const kh_array* scales_up, const kh_array* biases_up,
+                         kh_optional_int group_size, kh_optional_int bits, const char* mode,
+                         kh_stream stream) {
+  const char* op = "quantized_gate_up";
+  kh::QmvArgs g, u;
+  bool eg = false, eu = false;
+  int rc = prepare_qmm(op, res, x, w_gate, scales_gate, biases_gate, true, group_size, bits, mode, stream,
+                       &g, &eg);
+  if (rc) return rc;
+  if ((rc = prepare_qmm(op, res, x, w_up, scales_up, biases_up, true, group_size, bits, mode, stream, &u,
+                        &eu)))
+    return rc;
+  if (eg || eu) return KH_OK;
+  if ((rc = check_device(op))) return rc;
+  if (fast_path(g, true) && fast_path(u, true) && gemv_path(g) && g.sdt == u.sdt) {
+    const hipError_t e = kh::launch_gemv_gate_up(g, u);
+    return e == hipSuccess ? KH_OK : hip_fail(op, e);
+  }
+  // Composite: gate and up into intermediates of the result dtype (workspace
+  // buffer 1; the matmuls use buffer 0), then the activation.
+  const size_t esz = dtype_size(res->dtype), count = (size_t)g.M * g.N;
+  Workspace ws;
+  if (!workspace(g.stream, (2 * count * esz + 255) / 4 + 64, &ws, &rc, op, 1)) return rc;
+  char* gbuf = reinterpret_cast<char*>(ws.data);
+  char* ubuf = gbuf + (count * esz + 255) / 256 * 256;
+  g.out = gbuf;
+  u.out = ubuf;
+  if ((rc = run_qmm(op, g, true))) return rc;
+  if ((rc = run_qmm(op, u, true))) return rc;
+  const hipError_t e = kh::launch_silu_mul(gbuf, ubuf, res->data, res->dtype, (int64_t)count, g.stream);
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
 }
 

@@ -19,6 +19,8 @@ lazy evaluation, results are ready once that stream is synchronised.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -105,6 +107,52 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     _check(_lib.lib().kh_quantized_matmul(
         _desc(out, "res"), _desc(x, "x"), _packed(w), _desc(scales, "scales"),
         _desc(biases, "biases"), bool(transpose), _lib.opt(group_size), _lib.opt(bits),
+        mode.encode() if mode is not None else None, _stream_handle(x, stream)))
+    return out
+
+
+def _ptrs(descs):
+    P = ctypes.POINTER(_lib.KhArray)
+    arr = (P * len(descs))(*[ctypes.pointer(d) for d in descs])
+    return arr, descs  # keep the descriptors alive with the array
+
+
+def quantized_matmul_multi(x: torch.Tensor, parts, transpose: bool = True, group_size: int = 64,
+                           bits: int = 4, *, mode: str = "affine", out_dtype=None, outs=None,
+                           stream=None):
+    """[x @ dequantize(w_i, s_i, b_i)^T for (w_i, s_i, b_i) in parts], one
+    launch where the decode GEMV applies (the q/k/v projections)."""
+    if isinstance(out_dtype, str):
+        out_dtype = _NAMES[out_dtype]
+    if outs is None:
+        outs = []
+        for w, sc, _ in parts:
+            N = w.shape[0] if transpose else w.shape[-1] * (32 // bits)
+            od = out_dtype or result_dtype(x.dtype, sc.dtype)
+            outs.append(torch.empty((*x.shape[:-1], N), dtype=od, device=x.device))
+    res, k0 = _ptrs([_desc(o, "res") for o in outs])
+    ws, k1 = _ptrs([_packed(w) for w, _, _ in parts])
+    ss, k2 = _ptrs([_desc(sc, "scales") for _, sc, _ in parts])
+    bs, k3 = _ptrs([_desc(b, "biases") for _, _, b in parts])
+    _check(_lib.lib().kh_quantized_matmul_multi(
+        len(parts), res, _desc(x, "x"), ws, ss, bs, bool(transpose), _lib.opt(group_size),
+        _lib.opt(bits), mode.encode() if mode is not None else None, _stream_handle(x, stream)))
+    return outs
+
+
+def quantized_gate_up(x: torch.Tensor, gate, up, group_size: int = 64, bits: int = 4, *,
+                      mode: str = "affine", out_dtype=None, out: torch.Tensor | None = None,
+                      stream=None) -> torch.Tensor:
+    """silu(x @ gate^T) * (x @ up^T) with gate = (w, scales, biases), likewise up."""
+    if isinstance(out_dtype, str):
+        out_dtype = _NAMES[out_dtype]
+    if out is None:
+        od = out_dtype or result_dtype(x.dtype, gate[1].dtype)
+        out = torch.empty((*x.shape[:-1], gate[0].shape[0]), dtype=od, device=x.device)
+    _check(_lib.lib().kh_quantized_gate_up(
+        _desc(out, "res"), _desc(x, "x"), _packed(gate[0]), _desc(gate[1], "scales_gate"),
+        _desc(gate[2], "biases_gate"), _packed(up[0]), _desc(up[1], "scales_up"),
+        _desc(up[2], "biases_up"), _lib.opt(group_size), _lib.opt(bits),
         mode.encode() if mode is not None else None, _stream_handle(x, stream)))
     return out
 

@@ -19,6 +19,7 @@ Reference semantics followed (paths relative to the reference repo):
   crates/kiln-mlx/src/ops.rs:249-254   take(a, indices, axis)
   crates/kiln-models/src/nn.rs:159-176 Embedding::lookup = take x3 + dequantize
   crates/kiln-models/src/config.rs:137-148 bits in {4,8}, group_size in {32,64,128}
+  crates/kiln-models/src/nn.rs:284-294 gated MLP input silu(gate(x)) * up(x)
 
 Arrays: numpy containers; bf16 and f16 values travel as uint16 bit patterns
 with an explicit dtype string ('bf16' | 'f16' | 'f32').
@@ -231,3 +232,16 @@ def result_dtype(xdt: str, sdt: str) -> str:
     """MLX promotion of (x, scales, biases): equal float types stay, mixing
     bf16 with f16 or anything with f32 gives f32."""
     return xdt if xdt == sdt else "f32"
+
+
+def silu_mul(g: np.ndarray, u: np.ndarray, dt: str) -> np.ndarray:
+    """silu(gate) * up as the gated MLP forms it (crates/kiln-models/src/
+    nn.rs:284-294: multiply(gate, sigmoid(gate)), then multiply by up), each
+    op's result an array of dtype dt: g and u (stored values of dt) ->
+    sigmoid evaluated in float32 and rounded to dt -> gate*sigmoid rounded ->
+    times up, rounded. Returns stored values of dt."""
+    gf, uf = to_f32(g, dt), to_f32(u, dt)
+    with np.errstate(over="ignore"):
+        sg = to_f32(from_f32(np.float32(1) / (np.float32(1) + np.exp(-gf)), dt), dt)
+    a = to_f32(from_f32(gf * sg, dt), dt)
+    return from_f32(a * uf, dt)

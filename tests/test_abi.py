@@ -152,3 +152,48 @@ def test_errors_are_thread_local():
     t.join()
     assert seen == [""]
     assert "bits=3" in _lib.last_error()
+
+
+def _pp(arrs):
+    P = ctypes.POINTER(_lib.KhArray)
+    return (P * len(arrs))(*[ctypes.pointer(a) for a in arrs])
+
+
+def test_fused_entry_points_validation():
+    L = _lib.lib()
+    res, x, w, s, b = good(M=2, N=32, K=128)
+    res2, _, w2, s2, b2 = good(M=2, N=16, K=128)
+    # n out of range / null part arrays
+    rc = L.kh_quantized_matmul_multi(0, _pp([res]), ctypes.byref(x), _pp([w]), _pp([s]), _pp([b]),
+                                     True, _lib.opt(64), _lib.opt(4), b"affine", None)
+    assert rc == 1 and "quantized_matmul_multi" in _lib.last_error()
+    # a bad part is reported with its shapes
+    bad_w = A(_lib.UINT32, (16, 8))  # K*bits/32 = 16 expected
+    rc = L.kh_quantized_matmul_multi(2, _pp([res, res2]), ctypes.byref(x), _pp([w, bad_w]),
+                                     _pp([s, s2]), _pp([b, b2]), True, _lib.opt(64), _lib.opt(4),
+                                     b"affine", None)
+    assert rc == 1 and "quantized_matmul_multi" in _lib.last_error()
+    # gate/up of different N cannot share one result
+    rc = L.kh_quantized_gate_up(ctypes.byref(res), ctypes.byref(x), ctypes.byref(w), ctypes.byref(s),
+                                ctypes.byref(b), ctypes.byref(w2), ctypes.byref(s2), ctypes.byref(b2),
+                                _lib.opt(64), _lib.opt(4), b"affine", None)
+    assert rc == 1 and "quantized_gate_up" in _lib.last_error()
+
+
+def test_fused_entry_points_without_gpu_report_no_device():
+    try:
+        import torch
+        has_gpu = torch.cuda.is_available()
+    except Exception:  # pragma: no cover
+        has_gpu = False
+    if has_gpu:
+        pytest.skip("a GPU is present")
+    L = _lib.lib()
+    res, x, w, s, b = good(M=2, N=32, K=128)
+    rc = L.kh_quantized_matmul_multi(2, _pp([res, res]), ctypes.byref(x), _pp([w, w]), _pp([s, s]),
+                                     _pp([b, b]), True, _lib.opt(64), _lib.opt(4), b"affine", None)
+    assert rc == 4
+    rc = L.kh_quantized_gate_up(ctypes.byref(res), ctypes.byref(x), ctypes.byref(w), ctypes.byref(s),
+                                ctypes.byref(b), ctypes.byref(w), ctypes.byref(s), ctypes.byref(b),
+                                _lib.opt(64), _lib.opt(4), b"affine", None)
+    assert rc == 4

@@ -297,3 +297,65 @@ def test_add_rejects_non_suffix_broadcast():
     a = torch.zeros((4, 8), dtype=torch.float16, device="cuda")
     with pytest.raises(ops.KilnError):
         ops.add(a, torch.zeros((4,), dtype=torch.float16, device="cuda"))
+
+
+# ----------------------------------------------------------------- fused neighbours (q/k/v, gate/up)
+
+@pytest.mark.parametrize("M", [1, 3, 8, 9, 40])
+@pytest.mark.parametrize("bits,gs", [(4, 64), (8, 128)])
+def test_multi_equals_separate_calls(M, bits, gs):
+    """kh_quantized_matmul_multi (the q/k/v triple on one x, nn.rs:724-726)
+    returns, part by part, the bits of separate kh_quantized_matmul calls."""
+    K = 1024
+    shapes = [(256, K), (64, K), (64, K)]
+    parts, host_parts = [], []
+    for i, (N, _) in enumerate(shapes):
+        L = make_linear_numpy(N, K, gs, "q4" if bits == 4 else "q8", seed=40 + i)
+        host_parts.append(L)
+        parts.append((dev(L["w"]), dev(L["scales"], "f16"), dev(L["biases"], "f16")))
+    x = dev(make_x_numpy(M, K, seed=44), "bf16")
+    outs = ops.quantized_matmul_multi(x, parts, True, gs, bits, out_dtype="bf16")
+    for (w, s, b), o in zip(parts, outs):
+        ref = ops.quantized_matmul(x, w, s, b, True, gs, bits, out_dtype="bf16")
+        assert torch.equal(o.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 17, 64])
+@pytest.mark.parametrize("odt", ["bf16", "f16", "f32"])
+def test_gate_up_matches_oracle(oracle, M, odt):
+    """kh_quantized_gate_up = silu(x gate^T) * (x up^T) with the per-op
+    roundings of nn.rs:284-294 (oracle.silu_mul), within the matmul tolerance
+    of the oracle; and, on the fused decode launch, equal (to one unit in the
+    last place: expf) to separate calls followed by the same activation."""
+    N, K, gs, bits = 272, 2048, 64, 4
+    Lg = make_linear_numpy(N, K, gs, "q4", seed=50)
+    Lu = make_linear_numpy(N, K, gs, "q4", seed=51)
+    x = make_x_numpy(M, K, seed=52, xdt="bf16")
+    gate = (dev(Lg["w"]), dev(Lg["scales"], "f16"), dev(Lg["biases"], "f16"))
+    up = (dev(Lu["w"]), dev(Lu["scales"], "f16"), dev(Lu["biases"], "f16"))
+    y = host(ops.quantized_gate_up(dev(x, "bf16"), gate, up, gs, bits, out_dtype=odt))
+    g_ref = oracle.quantized_matmul(x, "bf16", Lg["w"], Lg["scales"], Lg["biases"], "f16", gs, bits, True, odt)
+    u_ref = oracle.quantized_matmul(x, "bf16", Lu["w"], Lu["scales"], Lu["biases"], "f16", gs, bits, True, odt)
+    ref = oracle.silu_mul(g_ref, u_ref, odt)
+    mx, mean = parity_metrics(oracle.to_f32(y, odt), oracle.to_f32(ref, odt))
+    assert mx <= 2e-2 and mean <= 1e-3, (mx, mean)
+    # separate device calls + the same activation on the host
+    gd = host(ops.quantized_matmul(dev(x, "bf16"), *gate, True, gs, bits, out_dtype=odt))
+    ud = host(ops.quantized_matmul(dev(x, "bf16"), *up, True, gs, bits, out_dtype=odt))
+    sep = oracle.to_f32(oracle.silu_mul(gd, ud, odt), odt).astype(np.float64)
+    # one unit of the 16-bit formats; for float32 a few units (device expf and
+    # the float32 chain against numpy)
+    ulp = 2.0 ** (-7 if odt == "bf16" else (-10 if odt == "f16" else -20))
+    assert np.all(np.abs(oracle.to_f32(y, odt) - sep) <= ulp * np.abs(sep) + 1e-30)
+
+
+def test_fused_entry_points_validate():
+    L = make_linear_numpy(64, 256, 64, "q4", seed=3)
+    w, s, b = dev(L["w"]), dev(L["scales"], "f16"), dev(L["biases"], "f16")
+    L2 = make_linear_numpy(32, 256, 64, "q4", seed=4)
+    w2, s2, b2 = dev(L2["w"]), dev(L2["scales"], "f16"), dev(L2["biases"], "f16")
+    x = dev(make_x_numpy(2, 256, seed=5), "bf16")
+    with pytest.raises(ops.KilnError, match="quantized_gate_up"):
+        ops.quantized_gate_up(x, (w, s, b), (w2, s2, b2), 64, 4, out_dtype="bf16")
+    with pytest.raises(ops.KilnError, match="quantized_matmul_multi"):
+        ops.quantized_matmul_multi(x, [(w, s, b)], True, 48, 4, out_dtype="bf16")

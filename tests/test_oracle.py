@@ -214,3 +214,29 @@ def test_take_out_of_range_and_negative(oracle):
     assert got[2].tolist() == [0, 0, 0, 0]
     assert got[3].tolist() == [0, 0, 0, 0]
     assert got[4].tolist() == a[0].tolist()
+
+
+# --------------------------------------------------------------------------- gated MLP activation
+
+def test_silu_mul_f32_is_the_closed_form(oracle):
+    rng = np.random.default_rng(5)
+    g = rng.standard_normal(4096).astype(np.float32) * 6
+    u = rng.standard_normal(4096).astype(np.float32)
+    got = oracle.silu_mul(g, u, "f32").astype(np.float64)
+    want = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    assert np.allclose(got, want, rtol=2e-6, atol=1e-30)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_silu_mul_special_values_and_rounding(oracle, dt):
+    g = oracle.from_f32(np.array([0.0, -0.0, 30.0, -30.0, 1.0, -1.0], np.float32), dt)
+    u = oracle.from_f32(np.array([3.0, 3.0, 2.0, 2.0, 1.0, 1.0], np.float32), dt)
+    got = oracle.to_f32(oracle.silu_mul(g, u, dt), dt)
+    assert got[0] == 0 and got[1] == 0          # silu(0) = 0
+    assert got[2] == 60.0                       # sigmoid(30) rounds to 1 in 16 bits
+    assert abs(got[3]) < 1e-9                   # silu(-30) ~ -2.8e-12
+    # silu(1) = 0.7310586, silu(-1) = -0.2689414, each rounded to dt
+    for i, v in ((4, 0.7310585786), (5, -0.2689414214)):
+        assert abs(got[i] - v) <= 2 ** (-8 if dt == "bf16" else -11) * abs(v) * 2
+    # rounding happens at each op: stored results are representable in dt
+    assert np.array_equal(oracle.from_f32(got, dt), oracle.silu_mul(g, u, dt))
