@@ -17,6 +17,8 @@
  *                           over a's leading dimensions.
  *   kh_quantized_matmul_multi  the q/k/v projections (nn.rs:724-726) on one x.
  *   kh_quantized_gate_up    silu(gate(x)) * up(x) of the gated MLP (nn.rs:284-294).
+ *   kh_gather_qmm           replaces mlx_gather_qmm (ops.rs:390-429), the MoE
+ *                           expert dispatch (moe.rs:124-176).
  *   kh_quantized_embedding  the fused form of Embedding::lookup
  *                           (nn.rs:159-176): three take(axis=0) calls
  *                           followed by dequantize, in one pass.
@@ -158,6 +160,24 @@ int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gat
                          const kh_array* w_up, const kh_array* scales_up,
                          const kh_array* biases_up, kh_optional_int group_size,
                          kh_optional_int bits, const char* mode, kh_stream stream);
+
+/* Quantized gather-matmul over expert stacks (mlx_gather_qmm with null
+ * lhs_indices, bound at crates/kiln-mlx/src/ops.rs:390-429; called by
+ * SwitchLinear::forward, crates/kiln-models/src/moe.rs:124-176, for the MoE
+ * expert dispatch of SwitchGlu, moe.rs:272-310):
+ *   batch = broadcast(x.shape[:-2], rhs_indices.shape)     (numpy rules)
+ *   res[b] = x[b] @ dequantize(w[e], scales[e], biases[e])^T,  e = rhs_indices[b]
+ * x [..., M, K] bfloat16|float16|float32; w [E, N, K*bits/32] uint32;
+ * scales/biases [E, N, K/gs]; rhs_indices uint32|int32; res [batch..., M, N].
+ * transpose must be true (Kiln's only use). Negative int32 ids count from
+ * the end; ids outside [-E, E) give zero rows. sorted_indices is the
+ * reference's scheduling hint and does not change results. Numerics per
+ * pair as kh_quantized_matmul's decode path (exact products) where it
+ * applies, else an exact float32 chain. */
+int kh_gather_qmm(kh_array* res, const kh_array* x, const kh_array* w, const kh_array* scales,
+                  const kh_array* biases, const kh_array* rhs_indices, bool transpose,
+                  kh_optional_int group_size, kh_optional_int bits, const char* mode,
+                  bool sorted_indices, kh_stream stream);
 
 /* res = dequantize(take(w, ids), take(scales, ids), take(biases, ids)):
  * the quantized embedding lookup. ids uint32|int32 of any shape; w [V, H*bits/32];

@@ -22,6 +22,7 @@ STATUS = {0: "KH_OK", 1: "KH_ERR_INVALID_ARGUMENT", 2: "KH_ERR_UNSUPPORTED",
 
 # Every symbol include/kiln_hip.h declares.
 EXPORTS = ("kh_quantized_matmul", "kh_quantized_matmul_multi", "kh_quantized_gate_up",
+           "kh_gather_qmm",
            "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add", "kh_last_error",
            "kh_version")
 
@@ -60,6 +61,8 @@ def lib() -> ctypes.CDLL:
         L.kh_quantized_matmul_multi.argtypes = [ctypes.c_int, PP, P, PP, PP, PP, ctypes.c_bool,
                                                 KhOptionalInt, KhOptionalInt, ctypes.c_char_p,
                                                 ctypes.c_void_p]
+        L.kh_gather_qmm.argtypes = [P, P, P, P, P, P, ctypes.c_bool, KhOptionalInt, KhOptionalInt,
+                                    ctypes.c_char_p, ctypes.c_bool, ctypes.c_void_p]
         L.kh_quantized_gate_up.argtypes = [P, P, P, P, P, P, P, P, KhOptionalInt, KhOptionalInt,
                                            ctypes.c_char_p, ctypes.c_void_p]
         L.kh_dequantize.argtypes = [P, P, P, P, KhOptionalInt, KhOptionalInt, ctypes.c_char_p,
@@ -69,6 +72,7 @@ def lib() -> ctypes.CDLL:
         L.kh_quantized_embedding.argtypes = [P, P, P, P, P, KhOptionalInt, KhOptionalInt,
                                              ctypes.c_char_p, ctypes.c_void_p]
         for f in ("kh_quantized_matmul", "kh_quantized_matmul_multi", "kh_quantized_gate_up",
+                  "kh_gather_qmm",
                   "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add"):
             getattr(L, f).restype = ctypes.c_int
         L.kh_last_error.restype = ctypes.c_char_p

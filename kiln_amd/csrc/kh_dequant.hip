@@ -157,6 +157,46 @@ __global__ void add_kernel(const void* __restrict__ a, int adt, const void* __re
   store_from_f32(res, rdt, i, load_as_f32(a, adt, i) + load_as_f32(b, bdt, i % nb));
 }
 
+// gather_qmm, any dtype / alignment / M: one thread per output column n,
+// pairs x rows over grid.y; float32 fma chain in k order (as the oracle).
+template <int BITS>
+__global__ void gather_generic_kernel(const void* __restrict__ x, int xdt, const uint32_t* __restrict__ w,
+                                      const void* __restrict__ scales, const void* __restrict__ biases,
+                                      int sdt, void* __restrict__ out, int odt, int M, int N, int K,
+                                      int gs, GatherArgs g) {
+  constexpr int CPW = 32 / BITS;
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t WR = K / CPW, G = K / gs;
+  for (int64_t pm = blockIdx.y; pm < g.pairs * M; pm += gridDim.y) {
+    const int64_t pair = pm / M;
+    const int m = (int)(pm % M);
+    int64_t xo = 0, io = 0, rem = pair;
+    for (int d = g.nd - 1; d >= 0; --d) {
+      const int64_t c = rem % g.shape[d];
+      rem /= g.shape[d];
+      xo += c * g.xs[d];
+      io += c * g.is[d];
+    }
+    int64_t e = g.idx_signed ? (int64_t) static_cast<const int32_t*>(g.idx)[io]
+                             : (int64_t) static_cast<const uint32_t*>(g.idx)[io];
+    if (e < 0) e += g.E;
+    float acc = 0.f;
+    if (e >= 0 && e < g.E) {
+      const int64_t rn = e * N + n;  // row of the flattened [E*N, ...] stack
+      const uint32_t* row = w + rn * WR;
+      for (int k = 0; k < K; ++k) {
+        const float sc = load_as_f32(scales, sdt, rn * G + k / gs);
+        const float bi = load_as_f32(biases, sdt, rn * G + k / gs);
+        const float wv = fmaf(sc, (float)((row[k / CPW] >> (BITS * (k % CPW))) & MASK), bi);
+        acc = fmaf(load_as_f32(x, xdt, xo + (int64_t)m * K + k), wv, acc);
+      }
+    }
+    store_from_f32(out, odt, pm * N + n, acc);
+  }
+}
+
 __global__ void silu_mul_kernel(const void* __restrict__ g, const void* __restrict__ u,
                                 void* __restrict__ res, int dt, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -264,6 +304,19 @@ hipError_t launch_silu_mul(const void* g, const void* u, void* res, int dt, int6
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, g, u, res,
                      dt, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_generic(const QmvArgs& a, const GatherArgs& g) {
+  const int64_t rows = g.pairs * a.M;
+  if (rows == 0 || a.N == 0) return hipSuccess;
+  const dim3 block(128), grid((a.N + 127) / 128, (unsigned)(rows < 65535 ? rows : 65535));
+  if (a.bits == 4)
+    hipLaunchKernelGGL(gather_generic_kernel<4>, grid, block, 0, a.stream, a.x, a.xdt, (const uint32_t*)a.w,
+                       a.scales, a.biases, a.sdt, a.out, a.odt, a.M, a.N, a.K, a.gs, g);
+  else
+    hipLaunchKernelGGL(gather_generic_kernel<8>, grid, block, 0, a.stream, a.x, a.xdt, (const uint32_t*)a.w,
+                       a.scales, a.biases, a.sdt, a.out, a.odt, a.M, a.N, a.K, a.gs, g);
   return hipGetLastError();
 }
 

@@ -163,11 +163,27 @@ struct GemvParts {
   int nparts;
 };
 
+// Gather mode (gather_qmm): workgroup b computes rows [rb*R, rb*R+R) of
+// pair p = b / nrb; pair p's batch coordinates over `shape` give the offset
+// of its [M, K] activation block in x (strides xs) and of its expert id in
+// idx (strides is); the expert selects w/scales/biases slice e of part 0
+// (strides ew, es). An id outside [-E, E) (negative ids count from the end)
+// gives zero rows.
+constexpr int kGatherMaxDims = 8;
+struct GemvGather {
+  const void* idx;
+  int idx_signed, E, nrb, nd;
+  int shape[kGatherMaxDims];
+  int64_t xs[kGatherMaxDims], is[kGatherMaxDims];
+  int64_t ew, es;  // words per expert in w; halves per expert in scales/biases
+};
+
 // RT rows per workgroup: R rows of one part, or (GU) R = RT/2 rows of the
 // gate and the same R rows of the up projection, stored as silu(gate)*up.
 template <int BITS, bool XBF16, bool SBF16, int M, int RT, int I, bool GU>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
-    const uint16_t* __restrict__ x, const GemvParts parts, int odt, int Mrows, int K, int cshift) {
+    const uint16_t* __restrict__ x, const GemvParts parts, const GemvGather gth, int odt, int Mrows,
+    int K, int cshift) {
   constexpr int R = RT;
   constexpr int CPC = 128 / BITS;  // codes per chunk
   constexpr int NP = CPC / 2;      // operand pairs per chunk
@@ -189,7 +205,40 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
   if (!GU)
     for (int i = 1; i < parts.nparts; ++i) part = (int)blockIdx.x >= parts.wg0[i] ? i : part;
   const int N = parts.N[part];
-  const int row0 = ((int)blockIdx.x - parts.wg0[part]) * RP;
+  int row0 = ((int)blockIdx.x - parts.wg0[part]) * RP;
+  // operand pointers of this workgroup (h = 1: the up projection under GU)
+  const uint16_t* xp = x;
+  const uint32_t* wp[2] = {parts.w[part], parts.w[GU ? 1 : part]};
+  const uint16_t* sp[2] = {parts.scales[part], parts.scales[GU ? 1 : part]};
+  const uint16_t* bp[2] = {parts.biases[part], parts.biases[GU ? 1 : part]};
+  void* outp = parts.out[part];
+  if (!GU && gth.idx != nullptr) {  // uniform
+    const int pair = (int)blockIdx.x / gth.nrb;
+    row0 = ((int)blockIdx.x % gth.nrb) * RP;
+    int64_t xo = 0, io = 0;
+    int rem = pair;
+    for (int d = gth.nd - 1; d >= 0; --d) {
+      const int c = rem % gth.shape[d];
+      rem /= gth.shape[d];
+      xo += c * gth.xs[d];
+      io += c * gth.is[d];
+    }
+    int64_t e = gth.idx_signed ? (int64_t) static_cast<const int32_t*>(gth.idx)[io]
+                               : (int64_t) static_cast<const uint32_t*>(gth.idx)[io];
+    if (e < 0) e += gth.E;
+    outp = static_cast<char*>(outp) + (int64_t)pair * Mrows * N * (odt == DT_F32 ? 4 : 2);
+    if (e < 0 || e >= gth.E) {  // uniform: zero rows, no loads
+      for (int t = tid; t < RP * Mrows; t += nth) {
+        const int r = t / Mrows, m = t % Mrows;
+        if (row0 + r < N) store_from_f32(outp, odt, (int64_t)m * N + row0 + r, 0.f);
+      }
+      return;
+    }
+    xp = x + xo;
+    wp[0] = wp[0] + e * gth.ew;
+    sp[0] = sp[0] + e * gth.es;
+    bp[0] = bp[0] + e * gth.es;
+  }
 
   int cidx[I];
   bool live[I];
@@ -203,14 +252,14 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
   // ---- issue every load: activations, codes, scale/bias halves. Each
   // address is a row base (uniform across the wave) plus a 32-bit lane
   // offset, the form the scalar-base global loads take.
-  const __amdgpu_buffer_rsrc_t bx = buffer_of(x);
+  const __amdgpu_buffer_rsrc_t bx = buffer_of(xp);
   // descriptors of the part (GU: [0] gate, [1] up)
   __amdgpu_buffer_rsrc_t bw[2], bs[2], bb[2];
 #pragma unroll
   for (int h = 0; h < (GU ? 2 : 1); ++h) {
-    bw[h] = buffer_of(parts.w[part + h]);
-    bs[h] = buffer_of(parts.scales[part + h]);
-    bb[h] = buffer_of(parts.biases[part + h]);
+    bw[h] = buffer_of(wp[h]);
+    bs[h] = buffer_of(sp[h]);
+    bb[h] = buffer_of(bp[h]);
   }
   u32x4 xr[I][M][NXV];
 #pragma unroll
@@ -317,7 +366,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
     for (int v = 1; v < W; ++v) s += red[v][tid];
     const int r = tid / M, m = tid % M;
     const int n = row0 + r;
-    if (n < N && m < Mrows) store_from_f32(parts.out[part], odt, (int64_t)m * N + n, s);
+    if (n < N && m < Mrows) store_from_f32(outp, odt, (int64_t)m * N + n, s);
   }
   if (GU && tid < NV / 2) {  // partial j = r*M + m: gate rows first, then up rows
     float g = red[0][tid], u = red[0][tid + NV / 2];
@@ -350,6 +399,8 @@ struct GemvLaunch {
   GemvParts parts;
   int total_wgs;
   bool gu;
+  GemvGather gth;  // idx == nullptr unless gather mode
+  int64_t pairs;   // gather mode: number of (activation block, expert) pairs
 };
 
 template <int BITS, bool XBF16, bool SBF16, int M, int R, int I>
@@ -360,14 +411,14 @@ hipError_t launch_one(const GemvLaunch& L, const GemvPlan& p) {
   if (L.gu) {
     if constexpr (2 * R * M <= 64)
       hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, 2 * R, I, true>), dim3(L.total_wgs),
-                         dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, L.parts, a.odt, a.M,
-                         a.K, cshift);
+                         dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, L.parts, L.gth, a.odt,
+                         a.M, a.K, cshift);
     else
       return hipErrorInvalidValue;
   } else {
     hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, R, I, false>), dim3(L.total_wgs),
-                       dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, L.parts, a.odt, a.M, a.K,
-                       cshift);
+                       dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, L.parts, L.gth, a.odt, a.M,
+                       a.K, cshift);
   }
   return hipGetLastError();
 }
@@ -428,6 +479,16 @@ hipError_t launch(GemvLaunch& L) {
   if (L.gu)  // the gate and up rows of a workgroup share its partial-sum lanes
     while (p.R > 2 && 2 * rows_launched(p, a.M) * (a.M <= 2 ? a.M : (a.M <= 4 ? 4 : 8)) > 64) p.R >>= 1;
   const int R = rows_launched(p, a.M);
+  if (L.gth.idx != nullptr) {
+    L.gth.nrb = (L.parts.N[0] + R - 1) / R;
+    const int64_t wgs = L.pairs * L.gth.nrb;
+    if (wgs > 0x7fffffff) return hipErrorInvalidValue;
+    L.total_wgs = (int)wgs;
+    L.parts.wg0[0] = 0;
+    const bool xbf16 = a.xdt == DT_BF16;
+    if (a.bits == 4) return xbf16 ? launch_x<4, true>(L, p) : launch_x<4, false>(L, p);
+    return xbf16 ? launch_x<8, true>(L, p) : launch_x<8, false>(L, p);
+  }
   L.total_wgs = 0;
   for (int i = 0; i < L.parts.nparts; ++i) {
     L.parts.wg0[i] = L.total_wgs;
@@ -461,7 +522,7 @@ int gemv_max_m(int K, int bits) {
 
 hipError_t launch_gemv(const QmvArgs& a) {
   if (a.M < 1 || a.M > gemv_max_m(a.K, a.bits)) return hipErrorInvalidValue;
-  GemvLaunch L{&a, {}, 0, false};
+  GemvLaunch L{&a, {}, 0, false, {}, 0};
   L.parts.nparts = 1;
   set_part(L.parts, 0, a);
   return launch(L);
@@ -470,7 +531,7 @@ hipError_t launch_gemv(const QmvArgs& a) {
 hipError_t launch_gemv_multi(const QmvArgs* a, int n) {
   if (n < 1 || n > kGemvMaxParts || a[0].M < 1 || a[0].M > gemv_max_m(a[0].K, a[0].bits))
     return hipErrorInvalidValue;
-  GemvLaunch L{&a[0], {}, 0, false};
+  GemvLaunch L{&a[0], {}, 0, false, {}, 0};
   L.parts.nparts = n;
   for (int i = 0; i < n; ++i) set_part(L.parts, i, a[i]);
   return launch(L);
@@ -478,10 +539,29 @@ hipError_t launch_gemv_multi(const QmvArgs* a, int n) {
 
 hipError_t launch_gemv_gate_up(const QmvArgs& gate, const QmvArgs& up) {
   if (gate.M < 1 || gate.M > gemv_max_m(gate.K, gate.bits) || gate.N != up.N) return hipErrorInvalidValue;
-  GemvLaunch L{&gate, {}, 0, true};
+  GemvLaunch L{&gate, {}, 0, true, {}, 0};
   L.parts.nparts = 2;
   set_part(L.parts, 0, gate);
   set_part(L.parts, 1, up);
+  return launch(L);
+}
+
+hipError_t launch_gemv_gather(const QmvArgs& a, const GatherArgs& g) {
+  if (a.M < 1 || a.M > gemv_max_m(a.K, a.bits) || g.nd > kGatherMaxDims) return hipErrorInvalidValue;
+  GemvLaunch L{&a, {}, 0, false, {}, g.pairs};
+  L.parts.nparts = 1;
+  set_part(L.parts, 0, a);
+  L.gth.idx = g.idx;
+  L.gth.idx_signed = g.idx_signed ? 1 : 0;
+  L.gth.E = g.E;
+  L.gth.nd = g.nd;
+  for (int d = 0; d < g.nd; ++d) {
+    L.gth.shape[d] = g.shape[d];
+    L.gth.xs[d] = g.xs[d];
+    L.gth.is[d] = g.is[d];
+  }
+  L.gth.ew = (int64_t)a.N * a.K * a.bits / 32;
+  L.gth.es = (int64_t)a.N * (a.K / a.gs);
   return launch(L);
 }
 

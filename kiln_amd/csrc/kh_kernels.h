@@ -34,6 +34,24 @@ hipError_t launch_gemv(const QmvArgs& a);
 // Up to 4 weight sets sharing x (and M, K, bits, group size, dtypes), one
 // launch: q/k/v projections.
 hipError_t launch_gemv_multi(const QmvArgs* a, int n);
+// gather_qmm over expert stacks: a.w/scales/biases hold E slices of [N, ..];
+// pair p (of `pairs`) uses activation block x + xoff(p) ([M, K]) and expert
+// idx[ioff(p)], writing out + p*M*N. Offsets come from p's coordinates over
+// `shape` (nd batch dims) times the strides xs (elements of x) and is
+// (elements of idx).
+struct GatherArgs {
+  const void* idx;
+  bool idx_signed;
+  int E;
+  int64_t pairs;
+  int nd;
+  int shape[8];
+  int64_t xs[8], is[8];
+};
+hipError_t launch_gemv_gather(const QmvArgs& a, const GatherArgs& g);
+// Any dtype/alignment/M: one thread per output, float32 fma chain.
+hipError_t launch_gather_generic(const QmvArgs& a, const GatherArgs& g);
+
 // gate.out = silu(x gate^T) * (x up^T) (silu_mul sequence), one launch;
 // gate.N == up.N.
 hipError_t launch_gemv_gate_up(const QmvArgs& gate, const QmvArgs& up);

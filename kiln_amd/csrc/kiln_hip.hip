@@ -447,6 +447,80 @@ int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gat
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
 }
 
+int kh_gather_qmm(kh_array* res, const kh_array* x, const kh_array* w, const kh_array* scales,
+                  const kh_array* biases, const kh_array* rhs_indices, bool transpose,
+                  kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,
+                  bool sorted_indices, kh_stream stream) {
+  (void)sorted_indices;  // a scheduling hint; results do not depend on it
+  const char* op = "gather_qmm";
+  int gs, bits, rc;
+  if ((rc = check_quant(op, group_size, bits_opt, mode, &gs, &bits))) return rc;
+  if ((rc = check_array(x, op, "x")) || (rc = check_array(rhs_indices, op, "rhs_indices"))) return rc;
+  if (!is_float(x->dtype))
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] x must be float16/bfloat16/float32, got %s", op, dtype_name(x->dtype));
+  if (x->ndim < 2) return fail(KH_ERR_INVALID_ARGUMENT, "[%s] x must have ndim >= 2, got %d", op, x->ndim);
+  if (rhs_indices->dtype != KH_UINT32 && rhs_indices->dtype != KH_INT32)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] rhs_indices must be uint32 or int32, got %s", op,
+                dtype_name(rhs_indices->dtype));
+  if (!transpose)
+    return fail(KH_ERR_UNSUPPORTED, "[%s] transpose=false is not supported (Kiln passes true)", op);
+  int64_t rows, cols;
+  if ((rc = check_packed(op, w, scales, biases, gs, bits, &rows, &cols))) return rc;
+  if (w->ndim != 3)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] w must be an expert stack [E, N, K*bits/32], got %s", op,
+                shape_str(w).c_str());
+  const int64_t E = w->shape[0], N = w->shape[1], K = cols;
+  const int64_t M = x->shape[x->ndim - 2];
+  if (x->shape[x->ndim - 1] != K)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] x %s has %lld input features but w %s expects %lld", op,
+                shape_str(x).c_str(), (long long)x->shape[x->ndim - 1], shape_str(w).c_str(), (long long)K);
+  // batch = broadcast(x.shape[:-2], rhs_indices.shape), numpy rules
+  const int xb = x->ndim - 2, ib = rhs_indices->ndim;
+  const int nd = xb > ib ? xb : ib;
+  if (nd > 8) return fail(KH_ERR_UNSUPPORTED, "[%s] more than 8 batch dimensions", op);
+  kh::GatherArgs g{};
+  g.idx = rhs_indices->data;
+  g.idx_signed = rhs_indices->dtype == KH_INT32;
+  g.E = (int)E;
+  g.nd = nd;
+  int64_t xstride = M * K, istride = 1, pairs = 1;
+  for (int d = nd - 1; d >= 0; --d) {
+    const int dx = d - (nd - xb), di = d - (nd - ib);
+    const int64_t sx = dx >= 0 ? x->shape[dx] : 1, si = di >= 0 ? rhs_indices->shape[di] : 1;
+    if (sx != si && sx != 1 && si != 1)
+      return fail(KH_ERR_INVALID_ARGUMENT, "[%s] x %s and rhs_indices %s do not broadcast", op,
+                  shape_str(x).c_str(), shape_str(rhs_indices).c_str());
+    const int64_t sd = sx == 1 ? si : sx;  // numpy: a size-1 dim takes the other (also 0)
+    if (sd > INT32_MAX) return fail(KH_ERR_UNSUPPORTED, "[%s] batch dimension beyond 2^31", op);
+    g.shape[d] = (int)sd;
+    g.xs[d] = sx == 1 ? 0 : xstride;
+    g.is[d] = si == 1 ? 0 : istride;
+    if (dx >= 0) xstride *= sx;
+    if (di >= 0) istride *= si;
+    pairs *= sd;
+  }
+  g.pairs = pairs;
+  kh_array want{};
+  want.dtype = res ? res->dtype : 0;
+  want.ndim = nd + 2;
+  for (int d = 0; d < nd; ++d) want.shape[d] = g.shape[d];
+  want.shape[nd] = M;
+  want.shape[nd + 1] = N;
+  if ((rc = check_result(op, res, want))) return rc;
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || E > INT32_MAX)
+    return fail(KH_ERR_UNSUPPORTED, "[%s] dimensions beyond 2^31 are not supported", op);
+  if (pairs == 0 || M == 0 || N == 0) return KH_OK;
+  if ((rc = check_device(op))) return rc;
+  kh::QmvArgs a{x->data, x->dtype, w->data, scales->data, biases->data, scales->dtype, res->data,
+                res->dtype, (int)M, (int)N, (int)K, gs, bits, static_cast<hipStream_t>(stream)};
+  hipError_t e;
+  if (fast_path(a, true) && gemv_path(a) && aligned16(x->data))
+    e = kh::launch_gemv_gather(a, g);
+  else
+    e = kh::launch_gather_generic(a, g);
+  return e == hipSuccess ? KH_OK : hip_fail(op, e);
+}
+
 int kh_dequantize(kh_array* res, const kh_array* w, const kh_array* scales, const kh_array* biases,
                   kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,
                   kh_stream stream) {

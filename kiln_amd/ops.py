@@ -140,6 +140,27 @@ def quantized_matmul_multi(x: torch.Tensor, parts, transpose: bool = True, group
     return outs
 
 
+def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               rhs_indices: torch.Tensor, transpose: bool = True, group_size: int = 64, bits: int = 4,
+               sorted_indices: bool = False, *, mode: str = "affine", out_dtype=None,
+               out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """res[b] = x[b] @ dequantize(w[e], ...)^T with e = rhs_indices[b] over
+    batch = broadcast(x.shape[:-2], rhs_indices.shape) (MoE expert dispatch)."""
+    if isinstance(out_dtype, str):
+        out_dtype = _NAMES[out_dtype]
+    if out is None:
+        batch = torch.broadcast_shapes(tuple(x.shape[:-2]), tuple(rhs_indices.shape))
+        od = out_dtype or result_dtype(x.dtype, scales.dtype)
+        out = torch.empty((*batch, x.shape[-2], w.shape[-2]), dtype=od, device=x.device)
+    idx = rhs_indices
+    idx_desc = _desc(idx, "rhs_indices", _lib.UINT32 if idx.dtype == torch.uint32 else None)
+    _check(_lib.lib().kh_gather_qmm(
+        _desc(out, "res"), _desc(x, "x"), _packed(w), _desc(scales, "scales"),
+        _desc(biases, "biases"), idx_desc, bool(transpose), _lib.opt(group_size), _lib.opt(bits),
+        mode.encode() if mode is not None else None, bool(sorted_indices), _stream_handle(x, stream)))
+    return out
+
+
 def quantized_gate_up(x: torch.Tensor, gate, up, group_size: int = 64, bits: int = 4, *,
                       mode: str = "affine", out_dtype=None, out: torch.Tensor | None = None,
                       stream=None) -> torch.Tensor:

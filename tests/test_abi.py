@@ -197,3 +197,46 @@ def test_fused_entry_points_without_gpu_report_no_device():
                                 ctypes.byref(b), ctypes.byref(w), ctypes.byref(s), ctypes.byref(b),
                                 _lib.opt(64), _lib.opt(4), b"affine", None)
     assert rc == 4
+
+
+def test_gather_qmm_validation():
+    L = _lib.lib()
+    E, N, K = 4, 32, 128
+
+    def call(res, x, w, s, b, idx, transpose=True):
+        return L.kh_gather_qmm(ctypes.byref(res), ctypes.byref(x), ctypes.byref(w), ctypes.byref(s),
+                               ctypes.byref(b), ctypes.byref(idx), transpose, _lib.opt(64), _lib.opt(4),
+                               b"affine", False, None)
+    w = A(_lib.UINT32, (E, N, K // 8))
+    s = A(_lib.FLOAT16, (E, N, K // 64))
+    x = A(_lib.BFLOAT16, (5, 1, 1, K))
+    idx = A(_lib.UINT32, (5, 3))
+    res = A(_lib.BFLOAT16, (5, 3, 1, N))
+    # 2-D weights are not an expert stack
+    assert call(res, x, A(_lib.UINT32, (N, K // 8)), A(_lib.FLOAT16, (N, 2)), A(_lib.FLOAT16, (N, 2)), idx) == 1
+    assert "expert stack" in _lib.last_error()
+    # float indices rejected
+    assert call(res, x, w, s, s, A(_lib.FLOAT32, (5, 3))) == 1 and "rhs_indices" in _lib.last_error()
+    # batch dims that do not broadcast
+    assert call(res, x, w, s, s, A(_lib.UINT32, (4, 3))) == 1 and "broadcast" in _lib.last_error()
+    # the result must have the broadcast batch shape
+    assert call(A(_lib.BFLOAT16, (5, 1, N)), x, w, s, s, idx) == 1 and "res" in _lib.last_error()
+    assert call(res, x, w, s, s, idx, transpose=False) == 2
+
+
+def test_gather_qmm_without_gpu_reports_no_device():
+    try:
+        import torch
+        has_gpu = torch.cuda.is_available()
+    except Exception:  # pragma: no cover
+        has_gpu = False
+    if has_gpu:
+        pytest.skip("a GPU is present")
+    L = _lib.lib()
+    w = A(_lib.UINT32, (4, 32, 16))
+    s = A(_lib.FLOAT16, (4, 32, 2))
+    rc = L.kh_gather_qmm(ctypes.byref(A(_lib.BFLOAT16, (6, 1, 32))), ctypes.byref(A(_lib.BFLOAT16, (6, 1, 128))),
+                         ctypes.byref(w), ctypes.byref(s), ctypes.byref(s),
+                         ctypes.byref(A(_lib.INT32, (6,))), True, _lib.opt(64), _lib.opt(4), b"affine",
+                         True, None)
+    assert rc == 4

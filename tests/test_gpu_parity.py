@@ -359,3 +359,99 @@ def test_fused_entry_points_validate():
         ops.quantized_gate_up(x, (w, s, b), (w2, s2, b2), 64, 4, out_dtype="bf16")
     with pytest.raises(ops.KilnError, match="quantized_matmul_multi"):
         ops.quantized_matmul_multi(x, [(w, s, b)], True, 48, 4, out_dtype="bf16")
+
+
+# ----------------------------------------------------------------- gather_qmm (MoE expert dispatch)
+
+def _experts(E, N, K, gs, bits, seed):
+    Ls = [make_linear_numpy(N, K, gs, "q4" if bits == 4 else "q8", seed=seed + e) for e in range(E)]
+    w = np.stack([L["w"] for L in Ls])
+    s = np.stack([L["scales"] for L in Ls])
+    b = np.stack([L["biases"] for L in Ls])
+    return w, s, b
+
+
+@pytest.mark.parametrize("layout", ["unsorted", "sorted"])
+@pytest.mark.parametrize("bits,gs", [(4, 64), (8, 32)])
+def test_gather_qmm_kiln_shapes(oracle, layout, bits, gs):
+    """SwitchLinear::forward's two call shapes (moe.rs:124-176, 272-310):
+    x [T,1,1,K] with indices [T,k] (no sort), and the sorted form x [T*k,1,K]
+    with indices [T*k]. Each pair equals kh_quantized_matmul on its expert's
+    slices, bit for bit, and the oracle to the decode bound."""
+    E, N, K, T, k = 6, 96, 512, 5, 3
+    w, s, b = _experts(E, N, K, gs, bits, seed=60)
+    rng = np.random.default_rng(61)
+    ids = rng.integers(0, E, (T, k)).astype(np.uint32)
+    xs = make_x_numpy(T, K, seed=62, xdt="bf16")
+    if layout == "unsorted":
+        x = dev(xs.reshape(T, 1, 1, K), "bf16")
+        idx = dev(ids)
+        pairs = [(t, j) for t in range(T) for j in range(k)]
+    else:
+        order = np.argsort(ids.reshape(-1), kind="stable")
+        x = dev(xs[order // k].reshape(T * k, 1, K), "bf16")
+        idx = dev(ids.reshape(-1)[order])
+        pairs = [(int(o) // k, int(o) % k) for o in order]
+    y = ops.gather_qmm(x, dev(w), dev(s, "f16"), dev(b, "f16"), idx, True, gs, bits, layout == "sorted",
+                       out_dtype="f32")
+    torch.cuda.synchronize()
+    yh = host(y).reshape(-1, N)
+    for p, (t, j) in enumerate(pairs):
+        e = int(ids[t, j])
+        L = dict(w=w[e], scales=s[e], biases=b[e])
+        xr = xs[t:t + 1]
+        got = yh[p:p + 1]
+        _check_f32(oracle, L, xr, gs, bits, "bf16", "f16", got, rel=EXACT_REL)
+        single = host(ops.quantized_matmul(dev(xr, "bf16"), dev(w[e]), dev(s[e], "f16"), dev(b[e], "f16"),
+                                           True, gs, bits, out_dtype="f32"))
+        assert np.array_equal(single.view(np.uint32), got.view(np.uint32)), p
+
+
+def test_gather_qmm_signed_and_out_of_range_ids(oracle):
+    E, N, K = 4, 64, 256
+    w, s, b = _experts(E, N, K, 64, 4, seed=70)
+    xs = make_x_numpy(4, K, seed=71, xdt="bf16")
+    ids = np.array([-1, 3, 7, -9], dtype=np.int32)  # -1 -> 3; 7 and -9 out of range
+    y = host(ops.gather_qmm(dev(xs.reshape(4, 1, K), "bf16"), dev(w), dev(s, "f16"), dev(b, "f16"),
+                            torch.from_numpy(ids).cuda(), True, 64, 4, out_dtype="f32")).reshape(4, N)
+    ref3 = host(ops.quantized_matmul(dev(xs[0:1], "bf16"), dev(w[3]), dev(s[3], "f16"), dev(b[3], "f16"),
+                                     True, 64, 4, out_dtype="f32"))
+    assert np.array_equal(y[0:1].view(np.uint32), ref3.view(np.uint32))
+    assert not y[2].any() and not y[3].any()
+
+
+@pytest.mark.parametrize("M,xdt", [(2, "bf16"), (12, "bf16"), (3, "f32")])
+def test_gather_qmm_rows_per_pair_and_fallback(oracle, M, xdt):
+    """M rows per pair through the decode kernel (M <= 8) or the exact
+    fallback (M > 8, float32 x): per pair, the oracle's bound (float32 x is
+    the oracle's own chain: bit-exact)."""
+    E, N, K, P = 3, 80, 256, 4
+    w, s, b = _experts(E, N, K, 64, 4, seed=80)
+    xs = make_x_numpy(P * M, K, seed=81, xdt=xdt).reshape(P, M, K)
+    ids = np.array([2, 0, 2, 1], dtype=np.uint32)
+    y = host(ops.gather_qmm(dev(xs, xdt if xdt != "f32" else None), dev(w), dev(s, "f16"), dev(b, "f16"),
+                            dev(ids), True, 64, 4, out_dtype="f32"))
+    for p in range(P):
+        e = int(ids[p])
+        L = dict(w=w[e], scales=s[e], biases=b[e])
+        ref = oracle.quantized_matmul_f32(xs[p], xdt, w[e], s[e], b[e], "f16", 64, 4, True)
+        if xdt == "f32":
+            assert np.array_equal(y[p].astype(np.float32).view(np.uint32), ref.astype(np.float32).view(np.uint32))
+        else:
+            _check_f32(oracle, L, xs[p], 64, 4, xdt, "f16", y[p], rel=EXACT_REL)
+
+
+def test_gather_qmm_empty_and_errors():
+    w, s, b = _experts(2, 32, 256, 64, 4, seed=90)
+    W = (dev(w), dev(s, "f16"), dev(b, "f16"))
+    x1 = dev(make_x_numpy(1, 256, seed=91).reshape(1, 1, 256), "bf16")
+    empty = ops.gather_qmm(x1, *W, torch.empty((0,), dtype=torch.int32, device="cuda"), True, 64, 4,
+                           out_dtype="bf16")
+    assert tuple(empty.shape) == (0, 1, 32)
+    x3 = dev(make_x_numpy(3, 256, seed=92).reshape(3, 1, 256), "bf16")
+    with pytest.raises(ops.KilnError, match="broadcast"):
+        ops.gather_qmm(x3, *W, torch.zeros((2,), dtype=torch.int32, device="cuda"), True, 64, 4,
+                       out=torch.empty((3, 1, 32), device="cuda", dtype=torch.bfloat16))
+    with pytest.raises(ops.KilnError, match="transpose=false"):
+        ops.gather_qmm(x3, *W, torch.zeros((3,), dtype=torch.int32, device="cuda"), False, 64, 4,
+                       out=torch.empty((3, 1, 32), device="cuda", dtype=torch.bfloat16))
