@@ -52,6 +52,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile", choices=["decode", "prefill", "traffic"], default=None,
+                    help="run one workload for a profiler and exit (no JSON line): the M=1 decode "
+                         "step, the M=2048 Llama-3-8B layer, or a copy of known size followed by "
+                         "gate-shape GEMV launches (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build runs the quantized linear path on a "
@@ -122,6 +126,9 @@ def main():
     shapes = LAYER_SHAPES["llama-3-8b"]
     layers = layer_copies(shapes, gs, "q4")
     copies = len(layers)
+    if args.profile:
+        profile_run(args.profile, torch, ops, layers, shapes, layer_fns, dev, gs, bits)
+        return
     step, per = layer_fns(layers, shapes, 1, gs, bits)
     reps = max(1, -(-args.steps // copies))
     wreps = max(1, -(-args.warmup // copies))
@@ -174,6 +181,34 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def profile_run(kind, torch, ops, layers, shapes, layer_fns, dev, gs, bits):
+    """Workloads for rocprofv3 (kernel trace or counters), eager launches."""
+    if kind == "decode":
+        step, _ = layer_fns(layers, shapes, 1, gs, bits)
+        for r in range(4 * len(layers)):
+            step(r % len(layers))
+    elif kind == "prefill":
+        step, _ = layer_fns(layers[:2], shapes, 2048, gs, bits)
+        for r in range(6):
+            step(r % 2)
+    else:
+        # a device-to-device copy of 256 MiB (reads and writes exactly that
+        # much: the calibration of FETCH_SIZE / WRITE_SIZE), then 12 launches
+        # of the gate-shape GEMV over distinct weight copies
+        a = torch.empty(64 << 20, dtype=torch.int32, device=dev).random_()
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        b.copy_(a)
+        torch.cuda.synchronize()
+        N, K = next((N, K) for n, N, K in shapes if n == "gate")
+        x = torch.randn((1, K), device=dev).bfloat16()
+        y = torch.empty((1, N), dtype=torch.bfloat16, device=dev)
+        for r in range(12):
+            W = layers[r % len(layers)]["gate"]
+            ops.quantized_matmul(x, W["w"], W["scales"], W["biases"], True, gs, bits, out=y)
+    torch.cuda.synchronize()
 
 
 def fused_step(torch, ops, layers, shapes, graph_us, dev, g, gs, bits, copies, reps):
