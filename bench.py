@@ -33,6 +33,9 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of `bench.py --profile traffic`:
+# 16,212.5 KiB read x 1.99976 + 56 KiB written, per launch of the gate GEMV
+GATE_TRAFFIC_BYTES = 33_257_515
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 600_000_000  # rotate over more distinct weight bytes than the 256 MB MALL
@@ -169,7 +172,10 @@ def main():
                    "weight_bytes_rotated": copies * sum(N * K // 2 for _, N, K in shapes)},
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     # HBM bytes per gate launch, FETCH_SIZE + WRITE_SIZE scaled by
+                     # what they read for a 256 MiB copy (x1.99976 and x1.0)
+                     "traffic": GATE_TRAFFIC_BYTES,
                      "kernel": "gemv_kernel<4,bf16,f16,M=1,R=8,I=1> at gate 14336x4096",
                      "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 3)},
         "per_shape_us": {k: round(v, 2) for k, v in per_shape_us.items()},
