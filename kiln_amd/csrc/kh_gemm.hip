@@ -105,6 +105,18 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 #ifndef KH_GEMM_ABL
 #define KH_GEMM_ABL 0  // tuning ablations: 1 no dequant/MFMA, 2 no scale loads, 3 no activation DMA/barrier
 #endif
+#ifndef KH_GEMM_ROT
+#define KH_GEMM_ROT 0  // tuning: rotate each workgroup's starting K chunk by n-tile
+#endif
+#ifndef KH_GEMM_NOACT
+#define KH_GEMM_NOACT 0  // tuning ablation: no activation DMA
+#endif
+#ifndef KH_GEMM_NOCODE
+#define KH_GEMM_NOCODE 0  // tuning ablation: no code loads
+#endif
+#ifndef KH_GEMM_CF
+#define KH_GEMM_CF 0  // tuning: issue each stage's code loads before its activation loads
+#endif
 #ifndef KH_GEMM_P
 #define KH_GEMM_P 0   // tuning: force the ring depth (0 = by tile size)
 #endif
@@ -173,6 +185,14 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   const int KB8 = K / 8;
   const int wpr = K * BITS / 32;           // words per row
   const int nchunks = (nst + P - 1) / P;
+  // Starting chunk rotated by n-tile: the workgroups resident on one XCD at a
+  // time (consecutive n-tiles of one m-tile) then read different K ranges of
+  // the shared activation panel instead of the same lines at once. The
+  // summation order of an output depends on its n-tile only.
+  const int roff = (KH_GEMM_ROT && nst % P == 0) ? (tn % nchunks) * P : 0;
+  auto rs = [&](int s) { const int r = s + roff; return r >= nst ? r - nst : r; };
+  const int rc = roff / P;
+  auto rchunk = [&](int c) { const int r = c + rc; return r >= nchunks ? r - nchunks : r; };
 
   // Rows of this lane's four code tiles (clamped: every load in bounds).
   int nrow[kNT];
@@ -193,7 +213,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
       for (int h = 0; h < LW; ++h) {
         const int code = kc + (BITS == 4 ? lg * 32 : h * 64 + lg * 16);
         const u32x4* src = reinterpret_cast<const u32x4*>(row + code * BITS / 32);
-        q[u][h] = KH_GEMM_NT ? __builtin_nontemporal_load(src) : *src;
+        if (!KH_GEMM_NOCODE) q[u][h] = KH_GEMM_NT ? __builtin_nontemporal_load(src) : *src;
       }
     }
   };
@@ -209,7 +229,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
       const int sl = s < SLOTS ? s : SLOTS - 1;
       const int m = sl >> 4, kb = (sl & 15) ^ (m & 15);
       const int mm = m0 + m < M ? m0 + m : M - 1;
-      if (KH_GEMM_ABL != 3 && (d * kWaves + wave) * 64 < SLOTS)  // wave-uniform
+      if (KH_GEMM_ABL != 3 && !KH_GEMM_NOACT && (d * kWaves + wave) * 64 < SLOTS)  // wave-uniform
         __builtin_amdgcn_global_load_lds(
             (const void*)(xh + (int64_t)mm * KB8 + kc8 + kb),
             (lds_void*)&As[buf][(d * kWaves + wave) * 64], 16, 0, 0);
@@ -218,7 +238,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   // Scale/bias chunk c into buffer c & 1: lane op i = (array, row, piece),
   // consecutive lanes -> consecutive pieces of one row (contiguous memory).
   auto load_scales = [&](int c) {
-    const int g0 = (k0 >> LGS) + c * SC::GC;
+    const int g0 = (k0 >> LGS) + rchunk(c) * SC::GC;
 #pragma unroll
     for (int d = 0; d < SC::OPS; ++d) {
       const int i = (d * kWaves + wave) * 64 + lane;
@@ -263,9 +283,15 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int t = 0; t < P - 1; ++t) {
-    load_acts(t, min(t, nst - 1));
-    __builtin_amdgcn_sched_barrier(0);
+#if KH_GEMM_CF
     load_codes(q[t], min(t, nst - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    load_acts(t, min(t, nst - 1));
+#else
+    load_acts(t, rs(min(t, nst - 1)));
+    __builtin_amdgcn_sched_barrier(0);
+    load_codes(q[t], rs(min(t, nst - 1)));
+#endif
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -274,14 +300,21 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     for (int p = 0; p < P; ++p) {
       const int st = c * P + p;
       if (p == 0)
-        waitcnt_vm<BASE>();
+        waitcnt_vm<(KH_GEMM_CF ? BASE - OPS : BASE)>();
       else
-        waitcnt_vm<BASE + SC::OPS>();
+        waitcnt_vm<(KH_GEMM_CF ? BASE - OPS : BASE) + SC::OPS>();
       if (KH_GEMM_ABL != 3) __builtin_amdgcn_s_barrier();
       const int pn = (p + P - 1) % P;  // slot and buffer of stage st + P - 1 (constant once unrolled)
+#if KH_GEMM_CF
+      load_codes(q[pn], min(st + P - 1, nst - 1));
+      __builtin_amdgcn_sched_barrier(0);
       load_acts(pn, min(st + P - 1, nst - 1));
       if (p == 0) load_scales(min(c + 1, nchunks - 1));
-      load_codes(q[pn], min(st + P - 1, nst - 1));
+#else
+      load_acts(pn, rs(min(st + P - 1, nst - 1)));
+      if (p == 0) load_scales(min(c + 1, nchunks - 1));
+      load_codes(q[pn], rs(min(st + P - 1, nst - 1)));
+#endif
       // The waits above rely on program order of the vector memory ops.
       __builtin_amdgcn_sched_barrier(0);
       if (KH_GEMM_ABL == 1 && st < nst) {
@@ -326,23 +359,60 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     }
   }
 
-  // ---- epilogue: D lane l holds column l%16, rows 4*(l/16)+i
+  // ---- epilogue. D lane l holds column l%16, rows 4*(l/16)+e of each 16x16
+  // tile. The tile goes through LDS (the activation ring, free once every
+  // wave is past its last stage and no prefetch is in flight) as float32
+  // rows of 256 columns, so that the stores leave as whole rows: 16-byte
+  // blocks XOR-swizzled by row so the scattered writes spread over the banks.
+  // Tiles taller than the ring holds go in passes of EP m-tiles.
+  constexpr int RING_BYTES = P * SLOTS * 16;
+  constexpr int EP = RING_BYTES / (16 * kBN * 4) < MT ? RING_BYTES / (16 * kBN * 4) : MT;
+  static_assert(EP >= 1 && MT % EP == 0, "epilogue passes");
+  float* T = reinterpret_cast<float*>(&As[0][0]);
+  auto tidx = [](int r, int c) {  // float index of (row r, column c) in T
+    return r * kBN + ((((c >> 2) ^ (((r >> 2) & 3) << 2))) << 2) + (c & 3);
+  };
+  // whole-block stores need 4 | N and 16-byte aligned base pointers
+  const bool vec = (N & 3) == 0 && (((uintptr_t)out | (uintptr_t)part) & 15) == 0;
 #pragma unroll
-  for (int i = 0; i < MT; ++i) {
+  for (int i0 = 0; i0 < MT; i0 += EP) {
+    __syncthreads();
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = m0 + i * 16 + 4 * lg + e;
-      if (m >= M) continue;
-      const float rs = rscale[m];
+    for (int i = i0; i < i0 + EP; ++i) {
 #pragma unroll
-      for (int u = 0; u < kNT; ++u) {
-        const int n = n0 + wave * 64 + u * 16 + col;
-        if (n >= N) continue;
-        const float v = acc[i][u][e] * rs;
-        if (nsplit == 1)
-          store_from_f32(out, odt, (int64_t)m * N + n, v);
-        else
-          part[((int64_t)sp * M + m) * N + n] = v;
+      for (int e = 0; e < 4; ++e) {
+        const int r = (i - i0) * 16 + 4 * lg + e;
+        const int m = m0 + i * 16 + 4 * lg + e;
+        const float rs = m < M ? rscale[m] : 0.f;
+#pragma unroll
+        for (int u = 0; u < kNT; ++u) T[tidx(r, wave * 64 + u * 16 + col)] = acc[i][u][e] * rs;
+      }
+    }
+    __syncthreads();
+    constexpr int BLOCKS = EP * 16 * (kBN / 4);  // 16-byte blocks of the pass
+#pragma unroll
+    for (int b0 = 0; b0 < BLOCKS; b0 += 64 * kWaves) {
+      const int b = b0 + tid, r = b / (kBN / 4), c = (b % (kBN / 4)) * 4;
+      const int m = m0 + i0 * 16 + r, n = n0 + c;
+      if (m >= M || n >= N) continue;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&T[tidx(r, c)]);
+      if (nsplit > 1) {
+        float* dst = part + ((int64_t)sp * M + m) * N + n;
+        if (vec) {
+          *reinterpret_cast<f32x4*>(dst) = v;
+        } else {
+          for (int k = 0; k < 4 && n + k < N; ++k) dst[k] = v[k];
+        }
+      } else if (vec && odt != DT_F32) {
+        const uint32_t lo = odt == DT_BF16 ? (f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16))
+                                           : (f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16));
+        const uint32_t hi = odt == DT_BF16 ? (f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16))
+                                           : (f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16));
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + (int64_t)m * N + n) = make_uint2(lo, hi);
+      } else if (vec) {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(out) + (int64_t)m * N + n) = v;
+      } else {
+        for (int k = 0; k < 4 && n + k < N; ++k) store_from_f32(out, odt, (int64_t)m * N + n + k, v[k]);
       }
     }
   }
