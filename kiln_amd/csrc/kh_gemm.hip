@@ -56,6 +56,28 @@ __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// LDS reads issued by inline asm, which the compiler's wait insertion does
+// not see: it treats an LDS read as possibly aliasing the direct-to-LDS
+// loads in flight and would put a full wait before it, exposing the LDS
+// latency at every read. The data read here was completed by the stage's
+// vmcnt wait and barrier. lds_wait_all() waits for these reads; ready(v)
+// orders a use of v after that wait.
+__device__ __forceinline__ uint32_t lds_u16_nowait(const void* p) {
+  uint32_t v;
+  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+  asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+__device__ __forceinline__ u32x4 lds_b128_nowait(const void* p) {
+  u32x4 v;
+  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+__device__ __forceinline__ void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::); }
+__device__ __forceinline__ void ready(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void ready(u32x4& v) { asm volatile("" : "+v"(v)); }
+
 // Pairs of codes as float16 (1024 + q) in both halves (exact for q < 1024),
 // in the pair order of permute_x: 4-bit word -> (c0,c4)(c1,c5)(c2,c6)(c3,c7);
 // 8-bit word pair -> (c0,c2)(c1,c3)(c4,c6)(c5,c7).
@@ -107,6 +129,12 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 #endif
 #ifndef KH_GEMM_ROT
 #define KH_GEMM_ROT 0  // tuning: rotate each workgroup's starting K chunk by n-tile
+#endif
+#ifndef KH_GEMM_NODQ
+#define KH_GEMM_NODQ 0  // tuning ablation: raw code pairs as the B operand (no dequantisation)
+#endif
+#ifndef KH_GEMM_NOMFMA
+#define KH_GEMM_NOMFMA 0  // tuning ablation: no MFMA
 #endif
 #ifndef KH_GEMM_NOACT
 #define KH_GEMM_NOACT 0  // tuning ablation: no activation DMA
@@ -213,7 +241,10 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
       for (int h = 0; h < LW; ++h) {
         const int code = kc + (BITS == 4 ? lg * 32 : h * 64 + lg * 16);
         const u32x4* src = reinterpret_cast<const u32x4*>(row + code * BITS / 32);
-        if (!KH_GEMM_NOCODE) q[u][h] = KH_GEMM_NT ? __builtin_nontemporal_load(src) : *src;
+        if (!KH_GEMM_NOCODE)
+          q[u][h] = KH_GEMM_NT ? __builtin_nontemporal_load(src) : *src;
+        else
+          q[u][h] = u32x4{(uint32_t)(lane * 7 + st), (uint32_t)(nrow[u] + st), (uint32_t)code, (uint32_t)kc};
       }
     }
   };
@@ -324,6 +355,39 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
                           (float)Ss[c & 1][u * 16 + col];
       } else if (st < nst) {  // uniform
         const unsigned char* sbuf = &Ss[c & 1][0];
+        // this lane's scale and bias for each of its code runs in the stage
+        // (one group per run), and the activation operands of step 0
+        uint32_t sv[kNT][LW], bv[kNT][LW];
+#pragma unroll
+        for (int u = 0; u < kNT; ++u)
+#pragma unroll
+          for (int h = 0; h < LW; ++h) {
+            const int gl = (p * kStage + (BITS == 4 ? lg * 32 : h * 64 + lg * 16)) >> LGS;
+            const int row = wave * 64 + u * 16 + col;
+            sv[u][h] = lds_u16_nowait(sbuf + SC::offset(0, row, gl));
+            bv[u][h] = lds_u16_nowait(sbuf + SC::offset(1, row, gl));
+          }
+        // activation operand (MFMA A layout: lane (row col, k-block lg)) of
+        // m-tile i for step j, from the swizzled slot p
+        u32x4 av[2][MT];
+        auto read_a = [&](u32x4 (&a)[MT], int j) {
+#pragma unroll
+          for (int i = 0; i < MT; ++i) {
+            const int m = i * 16 + col, kb = step_off<BITS>(j, lg) >> 3;
+            a[i] = lds_b128_nowait(&As[p][m * 16 + (kb ^ (m & 15))]);
+          }
+        };
+        read_a(av[0], 0);
+        lds_wait_all();
+#pragma unroll
+        for (int u = 0; u < kNT; ++u)
+#pragma unroll
+          for (int h = 0; h < LW; ++h) {
+            ready(sv[u][h]);
+            ready(bv[u][h]);
+          }
+#pragma unroll
+        for (int i = 0; i < MT; ++i) ready(av[0][i]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           u32x4 b[kNT];
@@ -334,25 +398,29 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
             const uint32_t q1 = BITS == 4 ? 0u : q[p][u][h][(j & 1) * 2 + 1];
             uint32_t r[4];
             pairs_1024<BITS>(q0, q1, mag, r);
-            // group of this lane's codes within the chunk
-            const int gl = (p * kStage + (BITS == 4 ? lg * 32 : h * 64 + lg * 16)) >> LGS;
-            const int row = wave * 64 + u * 16 + col;
-            const uint32_t sh = *reinterpret_cast<const uint16_t*>(sbuf + SC::offset(0, row, gl));
-            const uint32_t bh = *reinterpret_cast<const uint16_t*>(sbuf + SC::offset(1, row, gl));
-            const h2 s2 = KH_GEMM_ABL == 2 ? h2{(_Float16)0.01f, (_Float16)0.01f} : half_pair<SF16>(sh);
-            const h2 b2 = KH_GEMM_ABL == 2 ? h2{(_Float16)-0.08f, (_Float16)-0.08f} : half_pair<SF16>(bh);
+            const h2 s2 = KH_GEMM_ABL == 2 ? h2{(_Float16)0.01f, (_Float16)0.01f} : half_pair<SF16>(sv[u][h]);
+            const h2 b2 = KH_GEMM_ABL == 2 ? h2{(_Float16)-0.08f, (_Float16)-0.08f} : half_pair<SF16>(bv[u][h]);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              b[u][e] = __builtin_bit_cast(
+              b[u][e] = KH_GEMM_NODQ ? r[e] ^ sv[u][h] : __builtin_bit_cast(
                   uint32_t, __builtin_elementwise_fma(s2, __builtin_bit_cast(h2, r[e]) - k1024, b2));
           }
+          // operands of step j were read during step j-1 (or above)
+          if (j > 0) {
+            lds_wait_all();
 #pragma unroll
-          for (int i = 0; i < MT; ++i) {
-            const int m = i * 16 + col, kb = step_off<BITS>(j, lg) >> 3;
-            const u32x4 a = As[p][m * 16 + (kb ^ (m & 15))];
-#pragma unroll
-            for (int u = 0; u < kNT; ++u) acc[i][u] = mfma_f16(a, b[u], acc[i][u]);
+            for (int i = 0; i < MT; ++i) ready(av[j & 1][i]);
           }
+          if (j < 3) read_a(av[(j + 1) & 1], j + 1);
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int u = 0; u < kNT; ++u) {
+              if (KH_GEMM_NOMFMA)
+                acc[i][u][0] += __uint_as_float((av[j & 1][i][0] ^ b[u][0] ^ b[u][1] ^ b[u][2] ^ b[u][3]) & 0x3fffffffu);
+              else
+                acc[i][u] = mfma_f16(av[j & 1][i], b[u], acc[i][u]);
+            }
         }
       }
       __builtin_amdgcn_sched_barrier(0);
