@@ -145,6 +145,9 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 #ifndef KH_GEMM_CF
 #define KH_GEMM_CF 0  // tuning: issue each stage's code loads before its activation loads
 #endif
+#ifndef KH_GEMM_CAP
+#define KH_GEMM_CAP 256  // split-K target: workgroups per launch (one per CU)
+#endif
 #ifndef KH_GEMM_P
 #define KH_GEMM_P 0   // tuning: force the ring depth (0 = by tile size)
 #endif
@@ -506,13 +509,14 @@ GemmPlan plan_gemm(int M, int N, int K, int bits) {
   p.mt = mt;
   p.tiles_m = (M + 16 * mt - 1) / (16 * mt);
   p.tiles_n = (N + kBN - 1) / kBN;
-  // Split K while the launch has fewer than ~2 workgroups per CU and each
-  // slice keeps at least 4 stages. Below the largest tile the split depends
+  // Split K while the launch has fewer than one workgroup per CU (measured:
+  // splitting further only adds partial-sum traffic) and each slice keeps at
+  // least 4 stages. Below the largest tile the split depends
   // on (N, K, mt) only, so rows do not change with M inside one mt class.
   const int stages = K / kStage;
   const int tm = mt < kMaxMT ? 1 : p.tiles_m;
   int s = 1;
-  while (p.tiles_n * tm * s * 2 <= 512 && stages / (2 * s) >= 4) s *= 2;
+  while (p.tiles_n * tm * s * 2 <= KH_GEMM_CAP && stages / (2 * s) >= 4) s *= 2;
   p.nsplit = s;
   p.kslice = ((stages + s - 1) / s) * kStage;
   p.nsplit = (K + p.kslice - 1) / p.kslice;
