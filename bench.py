@@ -322,6 +322,24 @@ def run_sweep(torch, ops, l8_layers, l8_shapes, graph_us, layer_fns, layer_copie
     eb = T * (H * 4 // 8 + 2 * (H // 128) * 2 + 2 * H) + 4 * T
     out["embedding-gather-4096-zipf"] = {"us": round(us, 2), "gbs": round(eb / (us * 1e-6) / 1e9, 1)}
     del L4
+
+    # the affine quantizer (kh_quantize) on the gate shape, bf16 -> 4-bit gs64
+    # (reads the bf16 matrix, writes codes, scales and biases)
+    Nq, Kq = 14336, 4096
+    wsrc = [(torch.randn((Nq, Kq), device=dev) * 0.02).bfloat16() for _ in range(2)]
+    qo = [ops.quantize(w, 64, 4) for w in wsrc]
+    lib = ops._lib.lib()
+
+    def quant(c):
+        wq, s, b = qo[c]
+        ops._check(lib.kh_quantize(ops._desc(wq, "w_q", ops._lib.UINT32), ops._desc(s, "scales"),
+                                   ops._desc(b, "biases"), ops._desc(wsrc[c], "w"), ops._lib.opt(64),
+                                   ops._lib.opt(4), b"affine", ops._stream_handle(wsrc[c], None)))
+
+    us = graph_us(quant, 2, 20)
+    qb = Nq * Kq * 2 + Nq * Kq // 2 + 2 * Nq * (Kq // 64) * 2
+    out["quantize-14336x4096-bf16-q4-gs64"] = {"us": round(us, 2), "gbs": round(qb / (us * 1e-6) / 1e9, 1)}
+    del wsrc, qo
     return out
 
 

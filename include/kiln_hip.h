@@ -17,6 +17,9 @@
  *                           over a's leading dimensions.
  *   kh_quantized_matmul_multi  the q/k/v projections (nn.rs:724-726) on one x.
  *   kh_quantized_gate_up    silu(gate(x)) * up(x) of the gated MLP (nn.rs:284-294).
+ *   kh_quantize             mlx_quantize (mode "affine"), the arithmetic of the
+ *                           checkpoint conversion Kiln runs through mlx_lm
+ *                           convert (crates/kiln-jobs/src/quantize.rs:72-91).
  *   kh_gather_qmm           replaces mlx_gather_qmm (ops.rs:390-429), the MoE
  *                           expert dispatch (moe.rs:124-176).
  *   kh_quantized_embedding  the fused form of Embedding::lookup
@@ -125,6 +128,19 @@ int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
 /* res[r, k] = round(fma(f32(scales[r, k/gs]), f32(q[r, k]), f32(biases[r, k/gs])))
  * w [..., R, K*bits/32] -> res [..., R, K]; res dtype bfloat16|float16|float32
  * (MLX's default is the scales dtype, ops.rs:476-479 leaves it unset). */
+/* Affine quantization, as mlx_quantize(w, group_size, bits, "affine") of
+ * MLX v0.31.1 (Kiln reaches it through mlx_lm convert,
+ * crates/kiln-jobs/src/quantize.rs:72-91): w [..., K] float16|bfloat16|float32
+ * with K % group_size == 0 -> w_q uint32 [..., K*bits/32] (codes packed
+ * lowest bits first), scales and biases [..., K/group_size] of w's dtype.
+ * Per group, in float32: s = max((max - min) / (2^bits - 1), 1e-7), negated
+ * unless |min| > |max|; edge = the larger-magnitude extreme; q0 = round(edge
+ * / s); if q0 != 0, s = edge / q0 and b = edge, else b = 0; code =
+ * clamp(round((w - b) / s), 0, 2^bits - 1), rounding half away from zero. */
+int kh_quantize(kh_array* w_q, kh_array* scales, kh_array* biases, const kh_array* w,
+                kh_optional_int group_size, kh_optional_int bits, const char* mode,
+                kh_stream stream);
+
 int kh_dequantize(kh_array* res, const kh_array* w, const kh_array* scales,
                   const kh_array* biases, kh_optional_int group_size,
                   kh_optional_int bits, const char* mode, kh_stream stream);

@@ -22,7 +22,7 @@ STATUS = {0: "KH_OK", 1: "KH_ERR_INVALID_ARGUMENT", 2: "KH_ERR_UNSUPPORTED",
 
 # Every symbol include/kiln_hip.h declares.
 EXPORTS = ("kh_quantized_matmul", "kh_quantized_matmul_multi", "kh_quantized_gate_up",
-           "kh_gather_qmm",
+           "kh_gather_qmm", "kh_quantize",
            "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add", "kh_last_error",
            "kh_version")
 
@@ -67,12 +67,14 @@ def lib() -> ctypes.CDLL:
                                            ctypes.c_char_p, ctypes.c_void_p]
         L.kh_dequantize.argtypes = [P, P, P, P, KhOptionalInt, KhOptionalInt, ctypes.c_char_p,
                                     ctypes.c_void_p]
+        L.kh_quantize.argtypes = [P, P, P, P, KhOptionalInt, KhOptionalInt, ctypes.c_char_p,
+                                  ctypes.c_void_p]
         L.kh_take.argtypes = [P, P, P, ctypes.c_void_p]
         L.kh_add.argtypes = [P, P, P, ctypes.c_void_p]
         L.kh_quantized_embedding.argtypes = [P, P, P, P, P, KhOptionalInt, KhOptionalInt,
                                              ctypes.c_char_p, ctypes.c_void_p]
         for f in ("kh_quantized_matmul", "kh_quantized_matmul_multi", "kh_quantized_gate_up",
-                  "kh_gather_qmm",
+                  "kh_gather_qmm", "kh_quantize",
                   "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add"):
             getattr(L, f).restype = ctypes.c_int
         L.kh_last_error.restype = ctypes.c_char_p

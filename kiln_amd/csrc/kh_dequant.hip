@@ -209,6 +209,66 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v)
   if (i < n) p[i] = v;
 }
 
+// Affine quantization (mlx_quantize, mode "affine"; MLX v0.31.1's rule):
+// per group of GS values, in float32,
+//   s = max((hi - lo) / nb, 1e-7), negated unless |lo| > |hi|;
+//   edge = the larger-magnitude extreme; q0 = round(edge / s);
+//   if q0 != 0: s = edge / q0, b = edge, else b = 0;
+//   code = min(max(round((w - b) / s), 0), nb)      (round: half away from 0)
+// with s and b stored in w's dtype (round to nearest even) and the codes
+// computed from the float32 s and b. Lane t takes the 8 values 8t .. 8t+7
+// of the flattened rows (one output word at 4 bits, two at 8); the GS/8
+// lanes of a group reduce lo and hi by cross-lane exchange, and groups never
+// straddle a wave. Division is IEEE (the HIP default) and no product is
+// contracted, so results are bit-identical to a sequential float32 evaluation.
+template <int BITS, int GS>
+__global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ w, int wdt,
+                                                       uint32_t* __restrict__ wq,
+                                                       void* __restrict__ scales,
+                                                       void* __restrict__ biases, int64_t blocks) {
+#pragma clang fp contract(off)
+  constexpr int L = GS / 8;  // lanes per group
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= blocks) return;  // whole groups: blocks is a multiple of L
+  const float nb = (float)((1 << BITS) - 1);
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = load_as_f32(w, wdt, t * 8 + i);
+  float lo = v[0], hi = v[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) {
+    lo = fminf(lo, v[i]);
+    hi = fmaxf(hi, v[i]);
+  }
+#pragma unroll
+  for (int o = L / 2; o > 0; o >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, o));
+    hi = fmaxf(hi, __shfl_xor(hi, o));
+  }
+  float sc = fmaxf((hi - lo) / nb, 1e-7f);
+  const bool side = fabsf(lo) > fabsf(hi);
+  sc = side ? sc : -sc;
+  const float edge = side ? lo : hi;
+  const float q0 = roundf(edge / sc);
+  float bi = 0.f;
+  if (q0 != 0.f) {
+    sc = edge / q0;
+    bi = edge;
+  }
+  if (t % L == 0) {
+    store_from_f32(scales, wdt, t / L, sc);
+    store_from_f32(biases, wdt, t / L, bi);
+  }
+  uint32_t word[BITS / 4] = {};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float c = fminf(fmaxf(roundf((v[i] - bi) / sc), 0.f), nb);
+    word[i * BITS / 32] |= (uint32_t)c << (BITS * (i % (32 / BITS)));
+  }
+#pragma unroll
+  for (int j = 0; j < BITS / 4; ++j) wq[t * (BITS / 4) + j] = word[j];
+}
+
 inline unsigned blocks_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
 }  // namespace
@@ -317,6 +377,22 @@ hipError_t launch_gather_generic(const QmvArgs& a, const GatherArgs& g) {
   else
     hipLaunchKernelGGL(gather_generic_kernel<8>, grid, block, 0, a.stream, a.x, a.xdt, (const uint32_t*)a.w,
                        a.scales, a.biases, a.sdt, a.out, a.odt, a.M, a.N, a.K, a.gs, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize(const void* w, int wdt, void* wq, void* scales, void* biases,
+                           int64_t rows, int64_t K, int gs, int bits, hipStream_t stream) {
+  const int64_t blocks = rows * K / 8;
+  if (blocks == 0) return hipSuccess;
+  const dim3 grid(blocks_for(blocks, 256)), block(256);
+  uint32_t* q = static_cast<uint32_t*>(wq);
+#define KH_Q(B, G) hipLaunchKernelGGL((quantize_kernel<B, G>), grid, block, 0, stream, w, wdt, q, scales, biases, blocks)
+  if (bits == 4) {
+    if (gs == 32) KH_Q(4, 32); else if (gs == 64) KH_Q(4, 64); else KH_Q(4, 128);
+  } else {
+    if (gs == 32) KH_Q(8, 32); else if (gs == 64) KH_Q(8, 64); else KH_Q(8, 128);
+  }
+#undef KH_Q
   return hipGetLastError();
 }
 

@@ -100,6 +100,11 @@ hipError_t launch_embedding(const void* ids, bool ids_signed, int64_t T, const v
                             int64_t V, int64_t H, int gs, int bits, hipStream_t stream);
 
 // res[i] = silu_mul(g[i], u[i]) in dtype dt (g, u, res all of dtype dt).
+// Affine quantization of rows x K values (dtype wdt) into packed codes
+// [rows, K*bits/32] and scales/biases [rows, K/gs] of dtype wdt.
+hipError_t launch_quantize(const void* w, int wdt, void* wq, void* scales, void* biases,
+                           int64_t rows, int64_t K, int gs, int bits, hipStream_t stream);
+
 hipError_t launch_silu_mul(const void* g, const void* u, void* res, int dt, int64_t n,
                            hipStream_t stream);
 

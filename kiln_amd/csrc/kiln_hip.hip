@@ -521,6 +521,50 @@ int kh_gather_qmm(kh_array* res, const kh_array* x, const kh_array* w, const kh_
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
 }
 
+// mlx_quantize (mode "affine"): w [..., K] -> codes, scales, biases.
+int kh_quantize(kh_array* w_q, kh_array* scales, kh_array* biases, const kh_array* w,
+                kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,
+                kh_stream stream) {
+  const char* op = "quantize";
+  int gs, bits, rc;
+  if ((rc = check_quant(op, group_size, bits_opt, mode, &gs, &bits))) return rc;
+  if ((rc = check_array(w, op, "w")) || (rc = check_array(w_q, op, "w_q")) ||
+      (rc = check_array(scales, op, "scales")) || (rc = check_array(biases, op, "biases")))
+    return rc;
+  if (!is_float(w->dtype))
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] w must be float16/bfloat16/float32, got %s", op,
+                dtype_name(w->dtype));
+  if (w->ndim < 2)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] w must have ndim >= 2, got %d", op, w->ndim);
+  const int64_t K = w->shape[w->ndim - 1];
+  if (K % gs != 0)
+    return fail(KH_ERR_INVALID_ARGUMENT,
+                "[%s] the last dimension of w (%lld) must be divisible by group_size %d", op,
+                (long long)K, gs);
+  kh_array want_q = *w, want_s = *w;
+  want_q.dtype = KH_UINT32;
+  want_q.shape[w->ndim - 1] = K * bits / 32;
+  want_s.shape[w->ndim - 1] = K / gs;
+  const kh_array* outs[3] = {w_q, scales, biases};
+  const kh_array* wants[3] = {&want_q, &want_s, &want_s};
+  const char* names[3] = {"w_q", "scales", "biases"};
+  for (int o = 0; o < 3; ++o) {
+    bool same = outs[o]->dtype == wants[o]->dtype && outs[o]->ndim == wants[o]->ndim;
+    for (int i = 0; same && i < wants[o]->ndim; ++i) same = outs[o]->shape[i] == wants[o]->shape[i];
+    if (!same)
+      return fail(KH_ERR_INVALID_ARGUMENT, "[%s] %s is %s %s, expected %s %s", op, names[o],
+                  dtype_name(outs[o]->dtype), shape_str(outs[o]).c_str(),
+                  dtype_name(wants[o]->dtype), shape_str(wants[o]).c_str());
+  }
+  int64_t rows = 1;
+  for (int i = 0; i < w->ndim - 1; ++i) rows *= w->shape[i];
+  if (rows == 0 || K == 0) return KH_OK;
+  if ((rc = check_device(op))) return rc;
+  hipError_t e = kh::launch_quantize(w->data, w->dtype, w_q->data, scales->data, biases->data, rows,
+                                     K, gs, bits, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? KH_OK : hip_fail(op, e);
+}
+
 int kh_dequantize(kh_array* res, const kh_array* w, const kh_array* scales, const kh_array* biases,
                   kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,
                   kh_stream stream) {

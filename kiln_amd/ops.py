@@ -194,6 +194,23 @@ def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
     return out
 
 
+def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4, *, mode: str = "affine",
+             stream=None):
+    """mlx_quantize (affine): w [..., K] -> (w_q int32-held uint32 codes
+    [..., K*bits/32], scales, biases [..., K/group_size] of w's dtype)."""
+    lead, K = tuple(w.shape[:-1]), w.shape[-1] if w.dim() else 0
+    per = 32 // bits if bits in (4, 8) else 1
+    gs = group_size if group_size else 1
+    wq = torch.empty((*lead, K // per), dtype=torch.int32, device=w.device)
+    scales = torch.empty((*lead, K // gs), dtype=w.dtype, device=w.device)
+    biases = torch.empty_like(scales)
+    _check(_lib.lib().kh_quantize(
+        _desc(wq, "w_q", _lib.UINT32), _desc(scales, "scales"), _desc(biases, "biases"),
+        _desc(w, "w"), _lib.opt(group_size), _lib.opt(bits),
+        mode.encode() if mode is not None else None, _stream_handle(w, stream)))
+    return wq, scales, biases
+
+
 def take(a: torch.Tensor, indices: torch.Tensor, axis: int = 0, *,
          out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """Rows of `a` at `indices` along axis 0 (the embedding-lookup form)."""

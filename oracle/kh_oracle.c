@@ -146,6 +146,58 @@ void kho_dequantize(const uint32_t* w, const void* s, const void* b, int sdt, in
       store_f(out, odt, r * K + k, dq(w + r * wpr, s, b, sdt, r * G, k, gs, bits));
 }
 
+/* Affine quantization of rows of K values (dtype wdt) in groups of gs, as
+ * MLX v0.31.1 computes it (mlx_quantize, mode "affine"; the algorithm of
+ * MLX's affine_quantize, restated: Kiln itself quantizes through mlx_lm
+ * convert, crates/kiln-jobs/src/quantize.rs:72-91). Per group, in float32:
+ *   lo, hi = min, max of the group;  nb = 2^bits - 1
+ *   s = max((hi - lo) / nb, 1e-7);  side = |lo| > |hi|
+ *   s = side ? s : -s;  edge = side ? lo : hi
+ *   q0 = round(edge / s)                      (round: half away from zero)
+ *   s = q0 != 0 ? edge / q0 : s;  b = q0 != 0 ? edge : 0
+ *   code_k = min(max(round((w_k - b) / s), 0), nb)
+ * scales and biases are stored in wdt (round to nearest even); the codes use
+ * the float32 s and b. Codes are packed lowest bits first. */
+void kho_quantize(const void* w, int wdt, int64_t rows, int64_t K, int gs, int bits,
+                  uint32_t* wq, void* s_out, void* b_out) {
+  const float nb = (float)((1 << bits) - 1);
+  const int64_t G = K / gs, wpr = K * bits / 32;
+  const int per = 32 / bits;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t g = 0; g < G; ++g) {
+      const int64_t base = r * K + g * gs;
+      float lo = load_f(w, wdt, base), hi = lo;
+      for (int k = 1; k < gs; ++k) {
+        const float v = load_f(w, wdt, base + k);
+        lo = fminf(lo, v);
+        hi = fmaxf(hi, v);
+      }
+      float sc = fmaxf((hi - lo) / nb, 1e-7f);
+      const int side = fabsf(lo) > fabsf(hi);
+      sc = side ? sc : -sc;
+      const float edge = side ? lo : hi;
+      const float q0 = roundf(edge / sc);
+      float bi = 0.f;
+      if (q0 != 0.f) {
+        sc = edge / q0;
+        bi = edge;
+      }
+      store_f(s_out, wdt, r * G + g, sc);
+      store_f(b_out, wdt, r * G + g, bi);
+      for (int k = 0; k < gs; k += per) {
+        uint32_t word = 0;
+        for (int j = 0; j < per; ++j) {
+          const float v = roundf((load_f(w, wdt, base + k + j) - bi) / sc);
+          const float c = fminf(fmaxf(v, 0.f), nb);
+          word |= (uint32_t)c << (bits * j);
+        }
+        wq[r * wpr + (g * gs + k) / per] = word;
+      }
+    }
+  }
+}
+
 /* Float32 result of quantized_matmul (before output rounding), x [M,K].
  * transpose=1: w [N, K*bits/32], s/b [N, K/gs]; y[m,n] = sum_k x[m,k]*W[n,k].
  * transpose=0: w [K, N*bits/32], s/b [K, N/gs]; y[m,n] = sum_k x[m,k]*W[k,n].

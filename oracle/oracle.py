@@ -60,6 +60,7 @@ def lib():
         L.kho_qmm.argtypes = [vp, ci, vp, vp, vp, ci, i64, i64, i64, ci, ci, ci, vp, ci]
         L.kho_take.argtypes = [vp, i64, i64, vp, ci, i64, vp]
         L.kho_embedding.argtypes = [vp, ci, i64, vp, vp, vp, ci, i64, i64, ci, ci, vp, ci]
+        L.kho_quantize.argtypes = [vp, ci, i64, i64, ci, ci, vp, vp, vp]
         L.kho_f32_to_bf16.argtypes = [ctypes.c_float]
         L.kho_f32_to_bf16.restype = ctypes.c_uint16
         L.kho_f32_to_f16.argtypes = [ctypes.c_float]
@@ -226,6 +227,47 @@ def embedding(ids, w, s, b, sdt, gs, bits, odt=None) -> np.ndarray:
                         _p(np.ascontiguousarray(s)), _p(np.ascontiguousarray(b)), DT[sdt], V, H,
                         gs, bits, _p(out), DT[odt])
     return out
+
+
+def quantize(w: np.ndarray, wdt: str, gs: int, bits: int):
+    """Affine quantization of w [..., K] (stored bits of dtype wdt, or float32
+    values for "f32") -> (wq uint32 [..., K*bits/32], scales, biases [...,
+    K/gs] as stored bits of wdt). MLX v0.31.1's affine rule, restated in
+    oracle/kh_oracle.c (kho_quantize)."""
+    w = np.ascontiguousarray(w)
+    K = w.shape[-1]
+    rows = int(np.prod(w.shape[:-1])) if w.ndim > 1 else 1
+    wq = np.empty(w.shape[:-1] + (K * bits // 32,), dtype=np.uint32)
+    s = _out(w.shape[:-1] + (K // gs,), wdt)
+    b = _out(w.shape[:-1] + (K // gs,), wdt)
+    lib().kho_quantize(_p(w), DT[wdt], rows, K, gs, bits, _p(wq), _p(s), _p(b))
+    return wq, s, b
+
+
+def np_quantize(w: np.ndarray, wdt: str, gs: int, bits: int):
+    """numpy restatement of quantize (float32 arithmetic, round half away
+    from zero evaluated in float64, where x + 0.5 is exact)."""
+    v = to_f32(w, wdt).reshape(-1, gs)
+    nb = np.float32((1 << bits) - 1)
+    lo, hi = v.min(axis=1), v.max(axis=1)
+    sc = np.maximum((hi - lo) / nb, np.float32(1e-7)).astype(np.float32)
+    side = np.abs(lo) > np.abs(hi)
+    sc = np.where(side, sc, -sc).astype(np.float32)
+    edge = np.where(side, lo, hi).astype(np.float32)
+
+    def rnd(x):
+        x = np.asarray(x, dtype=np.float32).astype(np.float64)
+        return (np.sign(x) * np.floor(np.abs(x) + 0.5)).astype(np.float32)
+
+    q0 = rnd(edge / sc)
+    nz = q0 != 0
+    sc = np.where(nz, (edge / np.where(nz, q0, 1)).astype(np.float32), sc).astype(np.float32)
+    bi = np.where(nz, edge, np.float32(0)).astype(np.float32)
+    codes = np.clip(rnd((v - bi[:, None]) / sc[:, None]), 0, nb).astype(np.uint8)
+    shape = w.shape
+    wq = np_pack(codes.reshape(shape), bits)
+    gshape = shape[:-1] + (shape[-1] // gs,)
+    return wq, from_f32(sc.reshape(gshape), wdt), from_f32(bi.reshape(gshape), wdt)
 
 
 def result_dtype(xdt: str, sdt: str) -> str:

@@ -240,3 +240,44 @@ def test_gather_qmm_without_gpu_reports_no_device():
                          ctypes.byref(A(_lib.INT32, (6,))), True, _lib.opt(64), _lib.opt(4), b"affine",
                          True, None)
     assert rc == 4
+
+
+def _quantize(wq, s, b, w, gs=64, bits=4, mode=b"affine"):
+    return _lib.lib().kh_quantize(ctypes.byref(wq), ctypes.byref(s), ctypes.byref(b),
+                                  ctypes.byref(w), _lib.opt(gs), _lib.opt(bits), mode, None)
+
+
+def test_quantize_validation():
+    w = A(_lib.BFLOAT16, (6, 256))
+    good = (A(_lib.UINT32, (6, 32)), A(_lib.BFLOAT16, (6, 4)), A(_lib.BFLOAT16, (6, 4)), w)
+    # K not a multiple of the group size
+    assert _quantize(A(_lib.UINT32, (6, 12)), A(_lib.BFLOAT16, (6, 1)), A(_lib.BFLOAT16, (6, 1)),
+                     A(_lib.BFLOAT16, (6, 96)), gs=64) == 1
+    assert "divisible by group_size" in _lib.last_error()
+    # wrong packed width, wrong scale dtype, 1-d w, integer w, bad domain
+    assert _quantize(A(_lib.UINT32, (6, 16)), *good[1:]) == 1
+    assert "w_q is" in _lib.last_error()
+    assert _quantize(good[0], A(_lib.FLOAT16, (6, 4)), good[2], w) == 1
+    assert "scales is" in _lib.last_error()
+    assert _quantize(A(_lib.UINT32, (32,)), A(_lib.BFLOAT16, (4,)), A(_lib.BFLOAT16, (4,)),
+                     A(_lib.BFLOAT16, (256,))) == 1
+    assert "ndim >= 2" in _lib.last_error()
+    assert _quantize(good[0], good[1], good[2], A(_lib.UINT32, (6, 256))) == 1
+    assert _quantize(*good, bits=3) == 1
+    assert _quantize(*good, mode=b"mxfp4") in (1, 2)
+
+
+def test_quantize_without_gpu_reports_no_device():
+    try:
+        import torch
+        has_gpu = torch.cuda.is_available()
+    except Exception:  # pragma: no cover
+        has_gpu = False
+    if has_gpu:
+        pytest.skip("a GPU is present")
+    w = A(_lib.FLOAT32, (2, 3, 128))
+    assert _quantize(A(_lib.UINT32, (2, 3, 32)), A(_lib.FLOAT32, (2, 3, 1)),
+                     A(_lib.FLOAT32, (2, 3, 1)), w, gs=128, bits=8) == 4
+    # empty inputs succeed without touching the device
+    assert _quantize(A(_lib.UINT32, (0, 16)), A(_lib.FLOAT32, (0, 2)), A(_lib.FLOAT32, (0, 2)),
+                     A(_lib.FLOAT32, (0, 128))) == 0

@@ -455,3 +455,79 @@ def test_gather_qmm_empty_and_errors():
     with pytest.raises(ops.KilnError, match="transpose=false"):
         ops.gather_qmm(x3, *W, torch.zeros((3,), dtype=torch.int32, device="cuda"), False, 64, 4,
                        out=torch.empty((3, 1, 32), device="cuda", dtype=torch.bfloat16))
+
+
+# --------------------------------------------------------------------------- affine quantize
+
+def _quant_input(oracle, rows, K, gs, dt, seed):
+    rng = np.random.default_rng(seed)
+    v = (rng.standard_normal((rows, K)) * rng.uniform(0.001, 2, (rows, 1))).astype(np.float32)
+    v[0, :gs] = 0.0                      # all-zero group
+    v[1, :gs] = 0.375                    # constant group
+    v[2] = np.abs(v[2])                  # one-signed rows
+    v[3] = -np.abs(v[3])
+    if gs >= 32 and rows > 4:            # ties of the code rounding
+        v[4, :gs] = 0.0
+        v[4, 1], v[4, 2], v[4, 3] = 3.75, 3.625, 3.125
+    return oracle.from_f32(v, dt)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (4, 128), (8, 32), (8, 64), (8, 128)])
+def test_quantize_bit_exact(oracle, dt, bits, gs):
+    w = _quant_input(oracle, 37, 4 * gs + 2 * gs, gs, dt, seed=bits * 7 + gs)
+    got = ops.quantize(dev(w, dt), gs, bits)
+    want = oracle.quantize(w, dt, gs, bits)
+    for g, x in zip(got, want):
+        assert np.array_equal(host(g), x)
+
+
+@pytest.mark.gpu
+def test_quantize_leading_dims_and_round_trip(oracle):
+    gs, bits, dt = 64, 4, "bf16"
+    w = _quant_input(oracle, 2 * 3 * 5, 256, gs, dt, seed=11).reshape(2, 3, 5, 256)
+    wq, s, b = ops.quantize(dev(w, dt), gs, bits)
+    assert wq.shape == (2, 3, 5, 32) and s.shape == (2, 3, 5, 4)
+    want = oracle.quantize(w, dt, gs, bits)
+    for g, x in zip((wq, s, b), want):
+        assert np.array_equal(host(g), x)
+    # kh_dequantize of the result equals the oracle's dequantize of its own
+    # quantization, bit for bit
+    d = ops.dequantize(wq, s, b, gs, bits)
+    assert np.array_equal(host(d), oracle.dequantize(*want, dt, gs, bits, dt))
+
+
+@pytest.mark.gpu
+def test_quantize_feeds_quantized_matmul(oracle):
+    gs, bits, dt = 64, 4, "bf16"
+    w = _quant_input(oracle, 512, 1024, gs, dt, seed=5)
+    wq, s, b = ops.quantize(dev(w, dt), gs, bits)
+    x = oracle.from_f32(np.random.default_rng(6).standard_normal((3, 1024)).astype(np.float32), "bf16")
+    y = host(ops.quantized_matmul(dev(x, "bf16"), wq, s, b, True, gs, bits))
+    ref = oracle.quantized_matmul(x, "bf16", host(wq), host(s), host(b), dt, gs, bits, True, "bf16")
+    yf, rf = oracle.to_f32(y, "bf16"), oracle.to_f32(ref, "bf16")
+    assert np.abs(yf - rf).max() <= 2e-2 * np.abs(rf).max()
+
+
+@pytest.mark.gpu
+def test_quantize_full_gate_shape(oracle):
+    """BASELINE's gate shape 14336 x 4096, bf16 -> 4-bit gs64: rows quantize
+    independently, so a sample of rows is checked bit-exact against the oracle,
+    and every row against the round-trip bound."""
+    N, K, gs, bits = 14336, 4096, 64, 4
+    g = torch.Generator(device="cuda").manual_seed(3)
+    w = (torch.randn((N, K), generator=g, device="cuda") * 0.02).bfloat16()
+    wq, s, b = ops.quantize(w, gs, bits)
+    rows = np.random.default_rng(4).choice(N, 64, replace=False)
+    sel = torch.from_numpy(rows).cuda()
+    want = oracle.quantize(host(w[sel]), "bf16", gs, bits)
+    for got, x in zip((wq[sel], s[sel], b[sel]), want):
+        assert np.array_equal(host(got), x)
+    # round trip on the device: |dequant - w| <= |s| (half a step plus the
+    # bounded clipping of the far extreme) plus bf16 rounding of s and b
+    d = ops.dequantize(wq, s, b, gs, bits, out_dtype="f32")
+    err = (d - w.float()).abs().view(N, K // gs, gs)
+    sa = s.float().abs().unsqueeze(-1)
+    mag = w.float().abs().view(N, K // gs, gs).amax(-1, keepdim=True)
+    assert bool((err <= sa * 1.01 + 2.0 ** -8 * (15 * sa + mag)).all())

@@ -240,3 +240,92 @@ def test_silu_mul_special_values_and_rounding(oracle, dt):
         assert abs(got[i] - v) <= 2 ** (-8 if dt == "bf16" else -11) * abs(v) * 2
     # rounding happens at each op: stored results are representable in dt
     assert np.array_equal(oracle.from_f32(got, dt), oracle.silu_mul(g, u, dt))
+
+
+# --------------------------------------------------------------------------- affine quantize
+
+def _dq_f32(oracle, wq, s, b, dt, gs, bits):
+    codes = oracle.unpack(wq.reshape(-1, wq.shape[-1]), bits).astype(np.float64)
+    sv = np.repeat(oracle.to_f32(s, dt).reshape(codes.shape[0], -1).astype(np.float64), gs, axis=1)
+    bv = np.repeat(oracle.to_f32(b, dt).reshape(codes.shape[0], -1).astype(np.float64), gs, axis=1)
+    return codes, sv * codes + bv
+
+
+def test_quantize_known_answers(oracle):
+    # positive ramp 0, 0.25, ..., 3.75 (gs 32, 4-bit): the larger-magnitude
+    # extreme (3.75) is the edge, scale -0.25, bias 3.75, code 15 - k
+    k = np.arange(32) % 16
+    w = (k * 0.25).astype(np.float32)[None]
+    wq, s, b = oracle.quantize(w, "f32", 32, 4)
+    assert s.tolist() == [[-0.25]] and b.tolist() == [[3.75]]
+    assert oracle.unpack(wq, 4).tolist() == [(15 - k).tolist()]
+    # negative ramp 0, -0.5, ..., -7.5: edge -7.5, scale 0.5, code 15 - k
+    w = (-k * 0.5).astype(np.float32)[None]
+    wq, s, b = oracle.quantize(w, "f32", 32, 4)
+    assert s.tolist() == [[0.5]] and b.tolist() == [[-7.5]]
+    assert oracle.unpack(wq, 4).tolist() == [(15 - k).tolist()]
+    # ties round half away from zero: (3.625 - 3.75) / -0.25 = 0.5 -> 1,
+    # (3.125 - 3.75) / -0.25 = 2.5 -> 3 (round-half-even would give 0 and 2)
+    w = np.zeros(32, np.float32)
+    w[1], w[2], w[3] = 3.75, 3.625, 3.125
+    wq, s, b = oracle.quantize(w[None], "f32", 32, 4)
+    assert s.tolist() == [[-0.25]] and b.tolist() == [[3.75]]
+    assert oracle.unpack(wq, 4)[0, :4].tolist() == [15, 0, 1, 3]
+    # all-zero group: scale -1e-7 (the floor, negated), bias 0, codes 0
+    wq, s, b = oracle.quantize(np.zeros((1, 64), np.float32), "f32", 64, 8)
+    assert s[0, 0] == np.float32(-1e-7) and b.tolist() == [[0.0]] and not wq.any()
+    # constant group c: bias c and code 0 reproduce c exactly
+    wq, s, b = oracle.quantize(np.full((1, 64), 0.375, np.float32), "f32", 64, 4)
+    assert b.tolist() == [[0.375]] and not wq.any()
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (8, 64), (4, 128), (8, 128)])
+def test_quantize_round_trip_bound(oracle, dt, bits, gs):
+    rng = np.random.default_rng(bits * 1000 + gs)
+    v = (rng.standard_normal((37, 4 * gs)) * rng.uniform(0.01, 3, (37, 1))).astype(np.float32)
+    v[3] = np.abs(v[3])            # one-signed groups
+    v[4] = -np.abs(v[4])
+    w = oracle.from_f32(v, dt)
+    x = oracle.to_f32(w, dt).astype(np.float64)
+    wq, s, b = oracle.quantize(w, dt, gs, bits)
+    codes, rec = _dq_f32(oracle, wq, s, b, dt, gs, bits)
+    nb = (1 << bits) - 1
+    assert codes.min() >= 0 and codes.max() <= nb
+    g = x.reshape(x.shape[0], -1, gs)
+    sa = np.repeat(np.abs(oracle.to_f32(s, dt).astype(np.float64)), gs, axis=1)
+    rel = {"f32": 2.0 ** -22, "bf16": 2.0 ** -8, "f16": 2.0 ** -10}[dt]
+    # half the stored scale from the nearest code, plus the rounding of scale
+    # and bias to dt (scale error times up to nb codes, bias error). The
+    # scale is edge / round(edge / step): at most (nb/2 + 1/2) / (nb/2) steps.
+    mag = np.repeat(np.abs(g).max(axis=2), gs, axis=1)
+    step = np.repeat((g.max(axis=2) - g.min(axis=2)) / nb, gs, axis=1)
+    assert (sa <= step * (nb + 1) / nb * (1 + 2 * rel) + 1e-30).all()
+    # Rounding edge/step to an integer can also shrink the scale so that
+    # nb*|s| falls short of the group's range: the far extreme is then clipped
+    # to code nb, by at most that shortfall (the rule keeps 0 at an exact
+    # code instead of covering the whole range).
+    span = np.repeat(g.max(axis=2) - g.min(axis=2), gs, axis=1)
+    clip = np.maximum(span - nb * sa, 0)
+    # edge / step >= nb / 2, so the far code is at most nb + 1 before clipping
+    assert (clip <= sa * (1 + 4 * rel) + rel * mag).all()
+    bound = 0.5 * sa * (1 + rel) + clip + rel * (nb * sa + mag) * 1.01 + 1e-30
+    assert (np.abs(rec - x) <= bound).all()
+    # every group reaches both ends of the code range except where rounding
+    # the edge ratio moved the scale: the extremes map near 0 and nb
+    cg = codes.reshape(codes.shape[0], -1, gs)
+    assert (cg.min(axis=2) <= 1).all() and (cg.max(axis=2) >= nb - 1).all()
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("bits,gs", [(4, 32), (8, 64), (4, 128)])
+def test_quantize_c_equals_numpy_restatement(oracle, dt, bits, gs):
+    rng = np.random.default_rng(7 + bits + gs)
+    v = (rng.standard_normal((19, 3 * gs)) * 0.05).astype(np.float32)
+    v[0, :gs] = 0.0
+    v[1, :gs] = 0.25
+    w = oracle.from_f32(v, dt)
+    a = oracle.quantize(w, dt, gs, bits)
+    r = oracle.np_quantize(w, dt, gs, bits)
+    for x, y in zip(a, r):
+        assert np.array_equal(x, y)
