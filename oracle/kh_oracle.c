@@ -22,7 +22,11 @@
  *     transpose=false: y = x @ dequant(w)^T or x @ dequant(w), accumulated in
  *     float32 in increasing k order, rounded once to the output dtype;
  *   - Embedding::lookup (crates/kiln-models/src/nn.rs:159-176):
- *     take(w|scales|biases, ids, axis 0) then dequantize.
+ *     take(w|scales|biases, ids, axis 0) then dequantize;
+ *   - the affine quantize of the checkpoint conversion
+ *     (crates/kiln-jobs/src/quantize.rs:72-91 runs mlx_lm convert): kho_quantize,
+ *     pinned by known answers and round-trip bounds; its bit-level agreement
+ *     with MLX itself is "parity unpinned".
  *
  * MLX itself is absent (no install, no network); see the pinning tests for
  * what fixes each function independently.

@@ -20,6 +20,12 @@ Reference semantics followed (paths relative to the reference repo):
   crates/kiln-models/src/nn.rs:159-176 Embedding::lookup = take x3 + dequantize
   crates/kiln-models/src/config.rs:137-148 bits in {4,8}, group_size in {32,64,128}
   crates/kiln-models/src/nn.rs:284-294 gated MLP input silu(gate(x)) * up(x)
+  crates/kiln-jobs/src/quantize.rs:72-91 checkpoint conversion (mlx_lm
+                                       convert -> MLX's affine quantize), restated
+                                       as quantize / np_quantize; pinned by known
+                                       answers and round-trip bounds, while
+                                       bit-level agreement with MLX itself is
+                                       "parity unpinned" (MLX is not importable)
 
 Arrays: numpy containers; bf16 and f16 values travel as uint16 bit patterns
 with an explicit dtype string ('bf16' | 'f16' | 'f32').
