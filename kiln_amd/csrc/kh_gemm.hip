@@ -43,6 +43,7 @@ constexpr int kNT = 4;        // 16-column tiles per wave
 constexpr int kBN = kWaves * kNT * 16;  // 256
 constexpr int kXcds = 8;
 constexpr int kMaxMT = 8;     // largest m tile: 128 rows
+constexpr int kCUs = 256;     // MI355X compute units
 
 // s_waitcnt vmcnt(N) leaving expcnt and lgkmcnt unconstrained (gfx9
 // encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
@@ -148,6 +149,9 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 #ifndef KH_GEMM_CAP
 #define KH_GEMM_CAP 256  // split-K target: workgroups per launch (one per CU)
 #endif
+#ifndef KH_GEMM_TAIL
+#define KH_GEMM_TAIL 1  // run a partial last round of 128-row tiles as half-width workgroups
+#endif
 #ifndef KH_GEMM_P
 #define KH_GEMM_P 0   // tuning: force the ring depth (0 = by tile size)
 #endif
@@ -157,7 +161,7 @@ constexpr int ring_depth(int bits, int mt) {
 
 // Scale/bias chunk: the groups of P stages (P*128 codes) of every row of the
 // workgroup, copied to LDS by direct loads of SPIECE bytes.
-template <int GS, int P>
+template <int GS, int P, int BN>
 struct ScaleChunk {
   static constexpr int GC = P * kStage / GS;            // groups per row
   static constexpr int BYTES = GC * 2;                  // per row and array
@@ -169,26 +173,30 @@ struct ScaleChunk {
   static_assert(PIECES * SPIECE == BYTES && (2 * kStage / GS) % SPIECE == 0, "pieces tile stages");
   // Direct loads of fewer than 4 bytes still write one dword per lane in LDS.
   static constexpr int SSTRIDE = SPIECE < 4 ? 4 : SPIECE;     // LDS bytes per piece
-  static constexpr int LDS_BYTES = 2 * kBN * PIECES * SSTRIDE;  // one chunk buffer
+  static constexpr int LDS_BYTES = 2 * BN * PIECES * SSTRIDE;  // one chunk buffer
   // LDS byte offset of group g (within the chunk) of row `row`, array `arr`
   __device__ static constexpr int offset(int arr, int row, int g) {
-    return ((arr * kBN + row) * PIECES + g / (SPIECE / 2)) * SSTRIDE + (g % (SPIECE / 2)) * 2;
+    return ((arr * BN + row) * PIECES + g / (SPIECE / 2)) * SSTRIDE + (g % (SPIECE / 2)) * 2;
   }
-  static constexpr int OPS = 2 * kBN * PIECES / (64 * kWaves);  // direct loads per lane
+  static constexpr int OPS = 2 * BN * PIECES / (64 * kWaves);  // direct loads per lane
 };
 
-template <int BITS, bool SF16, int MT, int GS>
+template <int BITS, bool SF16, int MT, int GS, int NT>
 __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     const u32x4* __restrict__ xh, const float* __restrict__ rscale,
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, float* __restrict__ part, void* __restrict__ out,
-    int odt, int M, int N, int K, int kslice, int tiles_n, int tiles_m, int nsplit) {
+    int odt, int M, int N, int K, int kslice, int tiles_n, int tile0, int cnt, int nsplit) {
+  // NT 16-column MFMA tiles per wave: 4 (a 256-column tile) or 2 (half of
+  // one, for the last partial round of a launch)
+  constexpr int BN = kWaves * NT * 16;
+  constexpr int SUB = kBN / BN;           // workgroups per 256-column tile
   constexpr int BM = 16 * MT;
   constexpr int LW = BITS / 4;             // 16-byte code loads per lane per 16-row tile
   constexpr int SLOTS = 16 * BM;           // u32x4 activation slots per stage
   constexpr int DOPS = (SLOTS + 64 * kWaves - 1) / (64 * kWaves);  // activation loads per lane
   constexpr int P = ring_depth(BITS, MT);  // stages in flight
-  using SC = ScaleChunk<GS, P>;
+  using SC = ScaleChunk<GS, P, BN>;
   constexpr int LGS = __builtin_ctz(GS);
 
   __shared__ u32x4 As[P][SLOTS];
@@ -198,17 +206,20 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   const int lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, lg = lane >> 4;
 
-  // XCD-aware tile order: workgroup b runs on XCD b % 8; the tiles of one XCD
-  // are consecutive in (split, m-tile, n-tile) order, n fastest.
-  const int total = tiles_n * tiles_m * nsplit;
+  // XCD-aware tile order: workgroup b runs on XCD b % 8; the work items of
+  // one XCD are consecutive in (split, tile, part of tile) order, with tiles
+  // tile0 .. tile0+cnt-1 numbered m-tile-major, n fastest.
+  const int total = cnt * SUB * nsplit;
   const int per = (total + kXcds - 1) / kXcds;
   const int t = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
   if (t >= total) return;
-  const int tn = t % tiles_n;
-  const int tm = (t / tiles_n) % tiles_m;
-  const int sp = t / (tiles_n * tiles_m);
+  const int u0 = t % (cnt * SUB);
+  const int sp = t / (cnt * SUB);
+  const int tile = tile0 + u0 / SUB;
+  const int tn = tile % tiles_n;
+  const int tm = tile / tiles_n;
 
-  const int m0 = tm * BM, n0 = tn * kBN;
+  const int m0 = tm * BM, n0 = tn * kBN + (u0 % SUB) * BN;
   const int k0 = sp * kslice;
   const int k1 = min(K, k0 + kslice);
   const int nst = (k1 - k0) / kStage;      // K and kslice are multiples of kStage
@@ -226,19 +237,19 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   auto rchunk = [&](int c) { const int r = c + rc; return r >= nchunks ? r - nchunks : r; };
 
   // Rows of this lane's four code tiles (clamped: every load in bounds).
-  int nrow[kNT];
+  int nrow[NT];
 #pragma unroll
-  for (int u = 0; u < kNT; ++u) {
-    const int n = n0 + wave * 64 + u * 16 + col;
+  for (int u = 0; u < NT; ++u) {
+    const int n = n0 + wave * (NT * 16) + u * 16 + col;
     nrow[u] = n < N ? n : N - 1;
   }
 
   // ---- loaders (all in bounds: indices past the slice or the matrix are
   // clamped; what they fetch is never used)
-  auto load_codes = [&](u32x4 (&q)[kNT][LW], int st) {
+  auto load_codes = [&](u32x4 (&q)[NT][LW], int st) {
     const int kc = k0 + st * kStage;
 #pragma unroll
-    for (int u = 0; u < kNT; ++u) {
+    for (int u = 0; u < NT; ++u) {
       const uint32_t* row = w + (int64_t)nrow[u] * wpr;
 #pragma unroll
       for (int h = 0; h < LW; ++h) {
@@ -276,7 +287,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
 #pragma unroll
     for (int d = 0; d < SC::OPS; ++d) {
       const int i = (d * kWaves + wave) * 64 + lane;
-      const int piece = i % SC::PIECES, row = (i / SC::PIECES) % kBN, arr = i / (SC::PIECES * kBN);
+      const int piece = i % SC::PIECES, row = (i / SC::PIECES) % BN, arr = i / (SC::PIECES * BN);
       const int n = n0 + row < N ? n0 + row : N - 1;
       // a piece past the row's last group (only in the last chunk of a slice
       // whose stage count is not a multiple of P, or past K) reads the
@@ -294,13 +305,13 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   asm volatile("" : "+v"(mag));
   const h2 k1024 = h2{(_Float16)1024.f, (_Float16)1024.f};
 
-  f32x4 acc[MT][kNT];
+  f32x4 acc[MT][NT];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int u = 0; u < kNT; ++u) acc[i][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < NT; ++u) acc[i][u] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  u32x4 q[P][kNT][LW];  // code ring: slot p holds stage st with st % P == p
+  u32x4 q[P][NT][LW];  // code ring: slot p holds stage st with st % P == p
 
   // Issue order of vector-memory ops: scales(chunk 0); for t = 0..P-2:
   // activations(t), codes(t); then per stage st (p = st % P): wait for
@@ -310,7 +321,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   // indices keep this sequence free of branches, so the ops issued after
   // activations(st) are codes(st), P-2 stages of (activations, codes), and one
   // scale chunk unless p == 0: a compile-time count per p.
-  constexpr int OPS = LW * kNT;
+  constexpr int OPS = LW * NT;
   constexpr int BASE = OPS + (P - 2) * (DOPS + OPS);
   static_assert(BASE + SC::OPS < 64, "vmcnt holds 6 bits");
   load_scales(0);
@@ -353,20 +364,20 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
       __builtin_amdgcn_sched_barrier(0);
       if (KH_GEMM_ABL == 1 && st < nst) {
 #pragma unroll
-        for (int u = 0; u < kNT; ++u)
+        for (int u = 0; u < NT; ++u)
           acc[0][u][0] += __uint_as_float((q[p][u][0][0] ^ q[p][u][LW - 1][3]) & 0x3fffffffu) +
                           (float)Ss[c & 1][u * 16 + col];
       } else if (st < nst) {  // uniform
         const unsigned char* sbuf = &Ss[c & 1][0];
         // this lane's scale and bias for each of its code runs in the stage
         // (one group per run), and the activation operands of step 0
-        uint32_t sv[kNT][LW], bv[kNT][LW];
+        uint32_t sv[NT][LW], bv[NT][LW];
 #pragma unroll
-        for (int u = 0; u < kNT; ++u)
+        for (int u = 0; u < NT; ++u)
 #pragma unroll
           for (int h = 0; h < LW; ++h) {
             const int gl = (p * kStage + (BITS == 4 ? lg * 32 : h * 64 + lg * 16)) >> LGS;
-            const int row = wave * 64 + u * 16 + col;
+            const int row = wave * (NT * 16) + u * 16 + col;
             sv[u][h] = lds_u16_nowait(sbuf + SC::offset(0, row, gl));
             bv[u][h] = lds_u16_nowait(sbuf + SC::offset(1, row, gl));
           }
@@ -383,7 +394,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
         read_a(av[0], 0);
         lds_wait_all();
 #pragma unroll
-        for (int u = 0; u < kNT; ++u)
+        for (int u = 0; u < NT; ++u)
 #pragma unroll
           for (int h = 0; h < LW; ++h) {
             ready(sv[u][h]);
@@ -393,9 +404,9 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
         for (int i = 0; i < MT; ++i) ready(av[0][i]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          u32x4 b[kNT];
+          u32x4 b[NT];
 #pragma unroll
-          for (int u = 0; u < kNT; ++u) {
+          for (int u = 0; u < NT; ++u) {
             const int h = BITS == 4 ? 0 : (j >> 1);
             const uint32_t q0 = BITS == 4 ? q[p][u][0][j] : q[p][u][h][(j & 1) * 2];
             const uint32_t q1 = BITS == 4 ? 0u : q[p][u][h][(j & 1) * 2 + 1];
@@ -418,7 +429,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
 #pragma unroll
           for (int i = 0; i < MT; ++i)
 #pragma unroll
-            for (int u = 0; u < kNT; ++u) {
+            for (int u = 0; u < NT; ++u) {
               if (KH_GEMM_NOMFMA)
                 acc[i][u][0] += __uint_as_float((av[j & 1][i][0] ^ b[u][0] ^ b[u][1] ^ b[u][2] ^ b[u][3]) & 0x3fffffffu);
               else
@@ -437,11 +448,11 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   // blocks XOR-swizzled by row so the scattered writes spread over the banks.
   // Tiles taller than the ring holds go in passes of EP m-tiles.
   constexpr int RING_BYTES = P * SLOTS * 16;
-  constexpr int EP = RING_BYTES / (16 * kBN * 4) < MT ? RING_BYTES / (16 * kBN * 4) : MT;
+  constexpr int EP = RING_BYTES / (16 * BN * 4) < MT ? RING_BYTES / (16 * BN * 4) : MT;
   static_assert(EP >= 1 && MT % EP == 0, "epilogue passes");
   float* T = reinterpret_cast<float*>(&As[0][0]);
   auto tidx = [](int r, int c) {  // float index of (row r, column c) in T
-    return r * kBN + ((((c >> 2) ^ (((r >> 2) & 3) << 2))) << 2) + (c & 3);
+    return r * BN + ((((c >> 2) ^ (((r >> 2) & 3) << 2))) << 2) + (c & 3);
   };
   // whole-block stores need 4 | N and 16-byte aligned base pointers
   const bool vec = (N & 3) == 0 && (((uintptr_t)out | (uintptr_t)part) & 15) == 0;
@@ -456,14 +467,14 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
         const int m = m0 + i * 16 + 4 * lg + e;
         const float rs = m < M ? rscale[m] : 0.f;
 #pragma unroll
-        for (int u = 0; u < kNT; ++u) T[tidx(r, wave * 64 + u * 16 + col)] = acc[i][u][e] * rs;
+        for (int u = 0; u < NT; ++u) T[tidx(r, wave * (NT * 16) + u * 16 + col)] = acc[i][u][e] * rs;
       }
     }
     __syncthreads();
-    constexpr int BLOCKS = EP * 16 * (kBN / 4);  // 16-byte blocks of the pass
+    constexpr int BLOCKS = EP * 16 * (BN / 4);  // 16-byte blocks of the pass
 #pragma unroll
     for (int b0 = 0; b0 < BLOCKS; b0 += 64 * kWaves) {
-      const int b = b0 + tid, r = b / (kBN / 4), c = (b % (kBN / 4)) * 4;
+      const int b = b0 + tid, r = b / (BN / 4), c = (b % (BN / 4)) * 4;
       const int m = m0 + i0 * 16 + r, n = n0 + c;
       if (m >= M || n >= N) continue;
       const f32x4 v = *reinterpret_cast<const f32x4*>(&T[tidx(r, c)]);
@@ -520,6 +531,13 @@ GemmPlan plan_gemm(int M, int N, int K, int bits) {
   p.nsplit = s;
   p.kslice = ((stages + s - 1) / s) * kStage;
   p.nsplit = (K + p.kslice - 1) / p.kslice;
+  // 128-row tiles run one workgroup per CU. When the tiles fill a last round
+  // only partly (at most half), those tiles go to a second launch as two
+  // 128-column workgroups each, so the last round takes half the time. Each
+  // output element still accumulates over K in the same order: the rows are
+  // bit-identical to the full-width kernel's.
+  const int T = p.tiles_n * p.tiles_m, r = T % kCUs;
+  p.tail = (KH_GEMM_TAIL && mt == kMaxMT && p.nsplit == 1 && T > kCUs && r > 0 && r <= kCUs / 2) ? r : 0;
   return p;
 }
 
@@ -529,16 +547,28 @@ size_t gemm_partial_bytes(const GemmPlan& p, int M, int N) {
 
 bool gemm_supported(int K) { return K % kStage == 0; }
 
+template <int BITS, bool SF16, int MT, int GS, int NT>
+static hipError_t launch_range(const QmvArgs& a, const GemmPlan& p, const u32x4* xh,
+                               const float* rsc, float* part, int tile0, int cnt, int nsplit) {
+  const int total = cnt * (4 / NT) * nsplit;
+  const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
+  hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS, NT>), dim3(grid), dim3(64 * kWaves), 0,
+                     a.stream, xh, rsc, (const uint32_t*)a.w, (const uint16_t*)a.scales,
+                     (const uint16_t*)a.biases, part, a.out, a.odt, a.M, a.N, a.K, p.kslice,
+                     p.tiles_n, tile0, cnt, nsplit);
+  return hipGetLastError();
+}
+
 template <int BITS, bool SF16, int MT, int GS>
 static hipError_t launch_mt(const QmvArgs& a, const GemmPlan& p, const u32x4* xh, const float* rsc,
                             float* part) {
-  const int total = p.tiles_n * p.tiles_m * p.nsplit;
-  const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
-  hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS>), dim3(grid), dim3(64 * kWaves), 0, a.stream,
-                     xh, rsc, (const uint32_t*)a.w, (const uint16_t*)a.scales,
-                     (const uint16_t*)a.biases, part, a.out, a.odt, a.M, a.N, a.K, p.kslice,
-                     p.tiles_n, p.tiles_m, p.nsplit);
-  return hipGetLastError();
+  const int T = p.tiles_n * p.tiles_m;
+  hipError_t e = launch_range<BITS, SF16, MT, GS, 4>(a, p, xh, rsc, part, 0, T - p.tail, p.nsplit);
+  if constexpr (MT == kMaxMT) {
+    if (e == hipSuccess && p.tail > 0)
+      e = launch_range<BITS, SF16, MT, GS, 2>(a, p, xh, rsc, part, T - p.tail, p.tail, 1);
+  }
+  return e;
 }
 
 template <int BITS, bool SF16, int GS>

@@ -78,6 +78,7 @@ hipError_t launch_prep_x(const QmvArgs& a, void* xh, float* rsc);
 // in registers, deterministic split-K. The plan depends on M only through mt.
 struct GemmPlan {
   int mt, tiles_m, tiles_n, nsplit, kslice;
+  int tail;  // last tiles run as two half-width workgroups each (a second launch)
 };
 GemmPlan plan_gemm(int M, int N, int K, int bits);
 bool gemm_supported(int K);

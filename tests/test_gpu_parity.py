@@ -531,3 +531,24 @@ def test_quantize_full_gate_shape(oracle):
     sa = s.float().abs().unsqueeze(-1)
     mag = w.float().abs().view(N, K // gs, gs).amax(-1, keepdim=True)
     assert bool((err <= sa * 1.01 + 2.0 ** -8 * (15 * sa + mag)).all())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits,gs,odt", [(4, 64, "f32"), (8, 128, "bf16"), (4, 32, "f16")])
+def test_gemm_partial_last_round_runs_half_tiles(oracle, bits, gs, odt):
+    """17 column tiles x 16 row tiles of 128 = 272 tiles on 256 CUs: the last
+    16 run as half-width workgroups in a second launch. Rows there must match
+    the oracle and, bit for bit, the same rows computed by the full-width
+    kernel (x's last 128 rows repeat its first 128)."""
+    print(f"case gemm tail bits={bits} gs={gs} odt={odt}", flush=True)
+    M, N, K = 2048, 17 * 256, 256
+    L, x = _case(M, N, K, gs, bits, seed=31 + bits)
+    x[-128:] = x[:128]
+    y = _run(L, x, gs, bits, "bf16", "f16", odt)
+    assert np.array_equal(y[-128:], y[:128])
+    if odt == "f32":
+        _check_f32(oracle, L, x, gs, bits, "bf16", "f16", y)
+    else:
+        ref = oracle.quantized_matmul(x, "bf16", L["w"], L["scales"], L["biases"], "f16", gs, bits, True, odt)
+        mx, mean = parity_metrics(oracle.to_f32(y, odt), oracle.to_f32(ref, odt))
+        assert mx <= 2e-2 and mean <= 1e-3
