@@ -125,27 +125,6 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 #ifndef KH_GEMM_NT
 #define KH_GEMM_NT 1  // code loads marked non-temporal
 #endif
-#ifndef KH_GEMM_ABL
-#define KH_GEMM_ABL 0  // tuning ablations: 1 no dequant/MFMA, 2 no scale loads, 3 no activation DMA/barrier
-#endif
-#ifndef KH_GEMM_ROT
-#define KH_GEMM_ROT 0  // tuning: rotate each workgroup's starting K chunk by n-tile
-#endif
-#ifndef KH_GEMM_NODQ
-#define KH_GEMM_NODQ 0  // tuning ablation: raw code pairs as the B operand (no dequantisation)
-#endif
-#ifndef KH_GEMM_NOMFMA
-#define KH_GEMM_NOMFMA 0  // tuning ablation: no MFMA
-#endif
-#ifndef KH_GEMM_NOACT
-#define KH_GEMM_NOACT 0  // tuning ablation: no activation DMA
-#endif
-#ifndef KH_GEMM_NOCODE
-#define KH_GEMM_NOCODE 0  // tuning ablation: no code loads
-#endif
-#ifndef KH_GEMM_CF
-#define KH_GEMM_CF 0  // tuning: issue each stage's code loads before its activation loads
-#endif
 #ifndef KH_GEMM_CAP
 #define KH_GEMM_CAP 256  // split-K target: workgroups per launch (one per CU)
 #endif
@@ -227,14 +206,6 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   const int KB8 = K / 8;
   const int wpr = K * BITS / 32;           // words per row
   const int nchunks = (nst + P - 1) / P;
-  // Starting chunk rotated by n-tile: the workgroups resident on one XCD at a
-  // time (consecutive n-tiles of one m-tile) then read different K ranges of
-  // the shared activation panel instead of the same lines at once. The
-  // summation order of an output depends on its n-tile only.
-  const int roff = (KH_GEMM_ROT && nst % P == 0) ? (tn % nchunks) * P : 0;
-  auto rs = [&](int s) { const int r = s + roff; return r >= nst ? r - nst : r; };
-  const int rc = roff / P;
-  auto rchunk = [&](int c) { const int r = c + rc; return r >= nchunks ? r - nchunks : r; };
 
   // Rows of this lane's four code tiles (clamped: every load in bounds).
   int nrow[NT];
@@ -255,10 +226,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
       for (int h = 0; h < LW; ++h) {
         const int code = kc + (BITS == 4 ? lg * 32 : h * 64 + lg * 16);
         const u32x4* src = reinterpret_cast<const u32x4*>(row + code * BITS / 32);
-        if (!KH_GEMM_NOCODE)
-          q[u][h] = KH_GEMM_NT ? __builtin_nontemporal_load(src) : *src;
-        else
-          q[u][h] = u32x4{(uint32_t)(lane * 7 + st), (uint32_t)(nrow[u] + st), (uint32_t)code, (uint32_t)kc};
+        q[u][h] = KH_GEMM_NT ? __builtin_nontemporal_load(src) : *src;
       }
     }
   };
@@ -274,7 +242,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
       const int sl = s < SLOTS ? s : SLOTS - 1;
       const int m = sl >> 4, kb = (sl & 15) ^ (m & 15);
       const int mm = m0 + m < M ? m0 + m : M - 1;
-      if (KH_GEMM_ABL != 3 && !KH_GEMM_NOACT && (d * kWaves + wave) * 64 < SLOTS)  // wave-uniform
+      if ((d * kWaves + wave) * 64 < SLOTS)  // wave-uniform
         __builtin_amdgcn_global_load_lds(
             (const void*)(xh + (int64_t)mm * KB8 + kc8 + kb),
             (lds_void*)&As[buf][(d * kWaves + wave) * 64], 16, 0, 0);
@@ -283,7 +251,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   // Scale/bias chunk c into buffer c & 1: lane op i = (array, row, piece),
   // consecutive lanes -> consecutive pieces of one row (contiguous memory).
   auto load_scales = [&](int c) {
-    const int g0 = (k0 >> LGS) + rchunk(c) * SC::GC;
+    const int g0 = (k0 >> LGS) + c * SC::GC;
 #pragma unroll
     for (int d = 0; d < SC::OPS; ++d) {
       const int i = (d * kWaves + wave) * 64 + lane;
@@ -295,9 +263,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
       const int gp = min(g0 + piece * (SC::SPIECE / 2), G - SC::SPIECE / 2);
       const uint16_t* src = (arr ? biases : scales) + (int64_t)n * G + gp;
       lds_void* dst = (lds_void*)&Ss[c & 1][((d * kWaves + wave) * 64) * SC::SSTRIDE];
-      if (KH_GEMM_ABL != 2) {
-        __builtin_amdgcn_global_load_lds((const void*)src, dst, SC::SPIECE, 0, 0);
-      }
+      __builtin_amdgcn_global_load_lds((const void*)src, dst, SC::SPIECE, 0, 0);
     }
   };
 
@@ -328,15 +294,9 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int t = 0; t < P - 1; ++t) {
-#if KH_GEMM_CF
-    load_codes(q[t], min(t, nst - 1));
-    __builtin_amdgcn_sched_barrier(0);
     load_acts(t, min(t, nst - 1));
-#else
-    load_acts(t, rs(min(t, nst - 1)));
     __builtin_amdgcn_sched_barrier(0);
-    load_codes(q[t], rs(min(t, nst - 1)));
-#endif
+    load_codes(q[t], min(t, nst - 1));
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -345,29 +305,17 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     for (int p = 0; p < P; ++p) {
       const int st = c * P + p;
       if (p == 0)
-        waitcnt_vm<(KH_GEMM_CF ? BASE - OPS : BASE)>();
+        waitcnt_vm<BASE>();
       else
-        waitcnt_vm<(KH_GEMM_CF ? BASE - OPS : BASE) + SC::OPS>();
-      if (KH_GEMM_ABL != 3) __builtin_amdgcn_s_barrier();
+        waitcnt_vm<BASE + SC::OPS>();
+      __builtin_amdgcn_s_barrier();
       const int pn = (p + P - 1) % P;  // slot and buffer of stage st + P - 1 (constant once unrolled)
-#if KH_GEMM_CF
-      load_codes(q[pn], min(st + P - 1, nst - 1));
-      __builtin_amdgcn_sched_barrier(0);
       load_acts(pn, min(st + P - 1, nst - 1));
       if (p == 0) load_scales(min(c + 1, nchunks - 1));
-#else
-      load_acts(pn, rs(min(st + P - 1, nst - 1)));
-      if (p == 0) load_scales(min(c + 1, nchunks - 1));
-      load_codes(q[pn], rs(min(st + P - 1, nst - 1)));
-#endif
+      load_codes(q[pn], min(st + P - 1, nst - 1));
       // The waits above rely on program order of the vector memory ops.
       __builtin_amdgcn_sched_barrier(0);
-      if (KH_GEMM_ABL == 1 && st < nst) {
-#pragma unroll
-        for (int u = 0; u < NT; ++u)
-          acc[0][u][0] += __uint_as_float((q[p][u][0][0] ^ q[p][u][LW - 1][3]) & 0x3fffffffu) +
-                          (float)Ss[c & 1][u * 16 + col];
-      } else if (st < nst) {  // uniform
+      if (st < nst) {  // uniform
         const unsigned char* sbuf = &Ss[c & 1][0];
         // this lane's scale and bias for each of its code runs in the stage
         // (one group per run), and the activation operands of step 0
@@ -412,11 +360,11 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
             const uint32_t q1 = BITS == 4 ? 0u : q[p][u][h][(j & 1) * 2 + 1];
             uint32_t r[4];
             pairs_1024<BITS>(q0, q1, mag, r);
-            const h2 s2 = KH_GEMM_ABL == 2 ? h2{(_Float16)0.01f, (_Float16)0.01f} : half_pair<SF16>(sv[u][h]);
-            const h2 b2 = KH_GEMM_ABL == 2 ? h2{(_Float16)-0.08f, (_Float16)-0.08f} : half_pair<SF16>(bv[u][h]);
+            const h2 s2 = half_pair<SF16>(sv[u][h]);
+            const h2 b2 = half_pair<SF16>(bv[u][h]);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              b[u][e] = KH_GEMM_NODQ ? r[e] ^ sv[u][h] : __builtin_bit_cast(
+              b[u][e] = __builtin_bit_cast(
                   uint32_t, __builtin_elementwise_fma(s2, __builtin_bit_cast(h2, r[e]) - k1024, b2));
           }
           // operands of step j were read during step j-1 (or above)
@@ -429,12 +377,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
 #pragma unroll
           for (int i = 0; i < MT; ++i)
 #pragma unroll
-            for (int u = 0; u < NT; ++u) {
-              if (KH_GEMM_NOMFMA)
-                acc[i][u][0] += __uint_as_float((av[j & 1][i][0] ^ b[u][0] ^ b[u][1] ^ b[u][2] ^ b[u][3]) & 0x3fffffffu);
-              else
-                acc[i][u] = mfma_f16(av[j & 1][i], b[u], acc[i][u]);
-            }
+            for (int u = 0; u < NT; ++u) acc[i][u] = mfma_f16(av[j & 1][i], b[u], acc[i][u]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
