@@ -221,7 +221,7 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v)
 // lanes of a group reduce lo and hi by cross-lane exchange, and groups never
 // straddle a wave. Division is IEEE (the HIP default) and no product is
 // contracted, so results are bit-identical to a sequential float32 evaluation.
-template <int BITS, int GS>
+template <int BITS, int GS, bool VEC>
 __global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ w, int wdt,
                                                        uint32_t* __restrict__ wq,
                                                        void* __restrict__ scales,
@@ -232,8 +232,24 @@ __global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ 
   if (t >= blocks) return;  // whole groups: blocks is a multiple of L
   const float nb = (float)((1 << BITS) - 1);
   float v[8];
+  if (VEC && wdt != DT_F32) {  // 8 values: one 16-byte load
+    const u32x4 d = static_cast<const u32x4*>(w)[t];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = load_as_f32(w, wdt, t * 8 + i);
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t h = (d[i / 2] >> (16 * (i % 2))) & 0xffffu;
+      v[i] = wdt == DT_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+    }
+  } else if (VEC) {  // float32: two 16-byte loads
+    const f32x4 a = static_cast<const f32x4*>(w)[2 * t], b = static_cast<const f32x4*>(w)[2 * t + 1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[4 + i] = b[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = load_as_f32(w, wdt, t * 8 + i);
+  }
   float lo = v[0], hi = v[0];
 #pragma unroll
   for (int i = 1; i < 8; ++i) {
@@ -386,7 +402,16 @@ hipError_t launch_quantize(const void* w, int wdt, void* wq, void* scales, void*
   if (blocks == 0) return hipSuccess;
   const dim3 grid(blocks_for(blocks, 256)), block(256);
   uint32_t* q = static_cast<uint32_t*>(wq);
-#define KH_Q(B, G) hipLaunchKernelGGL((quantize_kernel<B, G>), grid, block, 0, stream, w, wdt, q, scales, biases, blocks)
+  const bool vec = (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+#define KH_Q(B, G)                                                                              \
+  do {                                                                                          \
+    if (vec)                                                                                    \
+      hipLaunchKernelGGL((quantize_kernel<B, G, true>), grid, block, 0, stream, w, wdt, q,      \
+                         scales, biases, blocks);                                               \
+    else                                                                                        \
+      hipLaunchKernelGGL((quantize_kernel<B, G, false>), grid, block, 0, stream, w, wdt, q,     \
+                         scales, biases, blocks);                                               \
+  } while (0)
   if (bits == 4) {
     if (gs == 32) KH_Q(4, 32); else if (gs == 64) KH_Q(4, 64); else KH_Q(4, 128);
   } else {

@@ -552,3 +552,14 @@ def test_gemm_partial_last_round_runs_half_tiles(oracle, bits, gs, odt):
         ref = oracle.quantized_matmul(x, "bf16", L["w"], L["scales"], L["biases"], "f16", gs, bits, True, odt)
         mx, mean = parity_metrics(oracle.to_f32(y, odt), oracle.to_f32(ref, odt))
         assert mx <= 2e-2 and mean <= 1e-3
+
+
+@pytest.mark.gpu
+def test_quantize_unaligned_input(oracle):
+    gs, bits = 32, 8
+    w = _quant_input(oracle, 6, 128, gs, "bf16", seed=9)
+    flat = torch.empty(w.size + 1, dtype=torch.bfloat16, device="cuda")
+    view = flat[1:].view(6, 128)                       # 2 bytes off 16-byte alignment
+    view.copy_(dev(w, "bf16"))
+    for g, x in zip(ops.quantize(view, gs, bits), oracle.quantize(w, "bf16", gs, bits)):
+        assert np.array_equal(host(g), x)
