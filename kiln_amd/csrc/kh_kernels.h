@@ -21,6 +21,12 @@ struct QmvArgs {
   hipStream_t stream;
 };
 
+// Small batches (M <= kSkinnyMaxM, K % 128 == 0): weights streamed once,
+// M rows on the matrix cores, exact products (kh_skinny.hip).
+constexpr int kSkinnyMaxM = 16;
+bool skinny_supported(int64_t M, int64_t N, int64_t K, int bits, int gs);
+hipError_t launch_skinny(const QmvArgs& a);
+
 // Largest M served by the decode kernel; larger M takes the prefill GEMM.
 constexpr int kDecodeMaxM = 16;
 

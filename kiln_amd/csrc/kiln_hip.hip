@@ -317,6 +317,12 @@ bool fast_path(const kh::QmvArgs& a, bool transpose) {
          aligned16(a.w);
 }
 
+#ifndef KH_SKINNY_MIN_M
+#define KH_SKINNY_MIN_M 5  // smallest M the skinny MFMA kernel takes over from the GEMV (measured)
+#endif
+bool skinny_path(const kh::QmvArgs& a) {
+  return a.M >= KH_SKINNY_MIN_M && kh::skinny_supported(a.M, a.N, a.K, a.bits, a.gs);
+}
 bool gemv_path(const kh::QmvArgs& a) {
   return a.M <= kh::gemv_max_m(a.K, a.bits) && kh::gemv_fits(a.M, a.N, a.K, a.bits, a.gs);
 }
@@ -331,6 +337,8 @@ int run_qmm(const char* op, const kh::QmvArgs& a, bool transpose) {
   // kernel, not a memset, so the call stays safe under graph capture).
   if (!fast_path(a, transpose)) {
     e = kh::launch_qmm_generic(a, transpose);
+  } else if (skinny_path(a)) {
+    e = kh::launch_skinny(a);
   } else if (gemv_path(a)) {
     e = kh::launch_gemv(a);
   } else if (kh::gemm_supported((int)K)) {
@@ -400,7 +408,8 @@ int kh_quantized_matmul_multi(int n, kh_array* const* res, const kh_array* x,
   }
   bool fused = n <= 4;
   for (int i = 0; i < n && fused; ++i)
-    fused = fast_path(a[i], transpose) && gemv_path(a[i]) && a[i].sdt == a[0].sdt && a[i].odt == a[0].odt;
+    fused = fast_path(a[i], transpose) && gemv_path(a[i]) && !skinny_path(a[i]) && a[i].sdt == a[0].sdt &&
+            a[i].odt == a[0].odt;
   if (fused) {
     const hipError_t e = kh::launch_gemv_multi(a.data(), n);
     return e == hipSuccess ? KH_OK : hip_fail(op, e);
@@ -428,7 +437,7 @@ int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gat
     return rc;
   if (eg || eu) return KH_OK;
   if ((rc = check_device(op))) return rc;
-  if (fast_path(g, true) && fast_path(u, true) && gemv_path(g) && g.sdt == u.sdt) {
+  if (fast_path(g, true) && fast_path(u, true) && gemv_path(g) && !skinny_path(g) && g.sdt == u.sdt) {
     const hipError_t e = kh::launch_gemv_gate_up(g, u);
     return e == hipSuccess ? KH_OK : hip_fail(op, e);
   }

@@ -51,7 +51,9 @@ def gemv_max_m(K: int, bits: int) -> int:
 def decode_regime(M: int, K: int, bits: int):
     """Which kernel (and tiling class) kh_quantized_matmul uses for a
     transpose=true call with bf16/f16 x and 16-bit scales: rows of the result
-    are bitwise identical for every M of one regime."""
+    are bitwise identical for every M of one regime (kiln_hip.hip, run_qmm)."""
+    if 5 <= M <= 16 and K % 128 == 0:
+        return ("skinny",)
     if M <= gemv_max_m(K, bits):
         return ("gemv",)
     if K % 128 == 0:
@@ -64,6 +66,7 @@ def decode_regime(M: int, K: int, bits: int):
 
 def exact_weights(M: int, K: int, bits: int) -> bool:
     """True where every dequantised weight enters the products unrounded
-    (the decode kernels); the GEMM kernels round each weight once to fp16."""
+    (the decode GEMV, the skinny MFMA kernel and qmv); the GEMM kernels round
+    each weight once to fp16."""
     r = decode_regime(M, K, bits)[0]
-    return r in ("gemv", "qmv")
+    return r in ("gemv", "skinny", "qmv")

@@ -12,7 +12,7 @@ import pytest
 
 from kiln_amd.workloads import make_linear_numpy, make_x_numpy
 
-from _util import gemv_max_m
+from _util import decode_regime
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 RUNNER = os.path.join(ROOT, "kiln_amd", "kiln_host_run")
@@ -116,13 +116,14 @@ def test_linear_embedding_head_from_checkpoint(oracle, tmp_path, sharded):
     assert np.mean(np.abs(lg - lref)) <= 1e-3 * np.mean(np.abs(lref))
 
     # probe_row_stability: row 0 stays bit-identical while M stays within the
-    # VALU decode kernel (M <= gemv_max_m), and first diverges after it
+    # kernel that serves M = 1, and first diverges where another takes over
     base = make_x_numpy(1, 64, seed=36, xdt="f16")
     (tmp_path / "b.bin").write_bytes(base.tobytes())
     rc, out, err = _job(tmp_path, model_dir=str(d), op="probe", prefix="model.embed_tokens", k=256,
                         input=str(tmp_path / "b.bin"), input_shape=[1, 1, 64], input_dtype="float16")
     assert rc == 0 and out["ok"], (out, err)
-    assert out["m"] == gemv_max_m(256, 4) + 1
+    first = next(m for m in range(2, 300) if decode_regime(m, 256, 4) != decode_regime(1, 256, 4))
+    assert out["m"] == first
 
 
 @pytest.mark.gpu
