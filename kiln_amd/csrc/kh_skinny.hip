@@ -45,17 +45,10 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// The scales or biases of one row for the GP groups of a piece (contiguous).
-template <int GP>
-struct SB {
-  uint16_t v[GP];
-};
-
-template <int BITS, int NTW, int GP>
+template <int BITS, int NTW>
 struct Piece {
   u32x4 q[NTW][BITS / 4];  // the lane's 32 codes per tile
-  u32x4 x[4];              // x[m, run .. run+31], permuted into code-pair order
-  SB<GP> s[NTW], b[NTW];
+  u32x4 x[4];              // x[m, run .. run+31]
 };
 
 template <int BITS, bool XBF16, bool SBF16, int GS, int NTW>
@@ -68,9 +61,13 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
   constexpr uint32_t MAG = XBF16 ? 0x43004300u : 0x64006400u;   // OFF in both halves
   constexpr uint32_t ONE = XBF16 ? 0x3F803F80u : 0x3C003C00u;   // 1.0 in both halves
   constexpr float OFF = SPLIT ? 17.f * 128.f : (XBF16 ? 128.f : 1024.f);
-  using P_t = Piece<BITS, NTW, GP>;
+  using P_t = Piece<BITS, NTW>;
+  constexpr int ROWS = 16 * NTW;
 
-  extern __shared__ float red[];  // [W][NTW][4][64]
+  // LDS: the scales and biases of the workgroup's rows for all of K
+  // ([2][ROWS][G] 16-bit values, loaded once), then the partial tiles of the
+  // cross-wave sum ([W][NTW][4][64] floats).
+  extern __shared__ __align__(16) unsigned char smem[];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
   const int col = lane & 15, kb = lane >> 4;
@@ -85,6 +82,9 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
   const bool mval = col < M;
   const u32x4* xr = reinterpret_cast<const u32x4*>(x + (int64_t)min(col, M - 1) * K);
 
+  uint16_t* sbl = reinterpret_cast<uint16_t*>(smem);
+  float* red = reinterpret_cast<float*>(smem + (size_t)2 * ROWS * G * 2);
+
   auto load = [&](P_t& P, int piece) {
     const int run = piece * kPiece + kb * 32;  // first code of the lane's run
 #pragma unroll
@@ -92,9 +92,6 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
       const u32x4* src = reinterpret_cast<const u32x4*>(w + (int64_t)nrow[t] * wpr + run * BITS / 32);
 #pragma unroll
       for (int h = 0; h < BITS / 4; ++h) P.q[t][h] = __builtin_nontemporal_load(src + h);
-      const int64_t sg = (int64_t)nrow[t] * G + piece * GP;
-      P.s[t] = *reinterpret_cast<const SB<GP>*>(scales + sg);
-      P.b[t] = *reinterpret_cast<const SB<GP>*>(biases + sg);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) P.x[j] = xr[(run >> 3) + j];  // row min(col, M-1)
@@ -105,7 +102,7 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
   for (int t = 0; t < NTW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const u32x4 ones = u32x4{ONE, ONE, ONE, ONE};
 
-  auto compute = [&](const P_t& P) {
+  auto compute = [&](const P_t& P, int piece) {
     f32x4 pa[NTW][GP], pb[NTW][GP], xs[GP];
 #pragma unroll
     for (int g = 0; g < GP; ++g) {
@@ -151,8 +148,9 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
     for (int t = 0; t < NTW; ++t)
 #pragma unroll
       for (int g = 0; g < GP; ++g) {
-        const float s = SBF16 ? bf16_bits_to_f32(P.s[t].v[g]) : f16_bits_to_f32(P.s[t].v[g]);
-        const float b = SBF16 ? bf16_bits_to_f32(P.b[t].v[g]) : f16_bits_to_f32(P.b[t].v[g]);
+        const int si = (t * 16 + col) * G + piece * GP + g;
+        const float s = SBF16 ? bf16_bits_to_f32(sbl[si]) : f16_bits_to_f32(sbl[si]);
+        const float b = SBF16 ? bf16_bits_to_f32(sbl[ROWS * G + si]) : f16_bits_to_f32(sbl[ROWS * G + si]);
         const float c = b - OFF * s;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -168,12 +166,34 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
   P_t A, B;
   const int p0 = wave * ppw;
   load(A, p0);
+  // the rows' scales and biases (rows n0 .. n0+ROWS-1 are consecutive, so
+  // each array is one contiguous run; rows past N are not loaded and their
+  // outputs are never stored)
+  {
+    const int nr = min(ROWS, N - n0);
+    const int64_t cnt = (int64_t)nr * G;
+    const uint16_t* src[2] = {scales + (int64_t)n0 * G, biases + (int64_t)n0 * G};
+    if ((G & 7) == 0) {
+      for (int64_t i = threadIdx.x; i < 2 * cnt / 8; i += blockDim.x) {
+        const int a = i >= cnt / 8;
+        const int64_t j = i - a * (cnt / 8);
+        reinterpret_cast<u32x4*>(sbl + a * ROWS * G)[j] = reinterpret_cast<const u32x4*>(src[a])[j];
+      }
+    } else {
+      for (int64_t i = threadIdx.x; i < 2 * cnt; i += blockDim.x) {
+        const int a = i >= cnt;
+        const int64_t j = i - a * cnt;
+        sbl[a * ROWS * G + j] = src[a][j];
+      }
+    }
+  }
+  __syncthreads();
   for (int i = 0; i < ppw; i += 2) {
     if (i + 1 < ppw) load(B, p0 + i + 1);
-    compute(A);
+    compute(A, p0 + i);
     if (i + 1 >= ppw) break;
     if (i + 2 < ppw) load(A, p0 + i + 2);
-    compute(B);
+    compute(B, p0 + i + 1);
   }
 
   // Sum the W partial tiles in wave order. D lane l holds rows 4*(l/16)+e,
@@ -214,10 +234,16 @@ SkinnyPlan plan_skinny(int N, int K, int bits, int gs) {
   return p;
 }
 
+// LDS of one workgroup: scales and biases of its rows, then the partial tiles.
+size_t skinny_lds(const SkinnyPlan& p, int64_t K, int gs) {
+  return (size_t)2 * 16 * p.ntw * (K / gs) * 2 + (size_t)p.W * p.ntw * 4 * 64 * sizeof(float);
+}
+constexpr size_t kSkMaxLds = 96 * 1024;  // keeps at least one workgroup per CU with room to spare
+
 template <int BITS, bool XBF16, bool SBF16, int GS, int NTW>
 hipError_t launch_t(const QmvArgs& a, const SkinnyPlan& p) {
   const int wgs = (a.N + 16 * NTW - 1) / (16 * NTW);
-  const size_t lds = (size_t)p.W * NTW * 4 * 64 * sizeof(float);
+  const size_t lds = skinny_lds(p, a.K, GS);
   hipLaunchKernelGGL((skinny_kernel<BITS, XBF16, SBF16, GS, NTW>), dim3(wgs), dim3(64 * p.W), lds,
                      a.stream, (const uint16_t*)a.x, (const uint32_t*)a.w,
                      (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.out, a.odt, a.M, a.N,
@@ -252,8 +278,10 @@ hipError_t launch_b(const QmvArgs& a, const SkinnyPlan& p) {
 
 bool skinny_supported(int64_t M, int64_t N, int64_t K, int bits, int gs) {
   const int64_t lim = (int64_t)1 << 31;
-  return M >= 1 && M <= kSkinnyMaxM && K % kPiece == 0 && N * K * bits / 8 < lim &&
-         M * K * 2 < lim && N * (K / gs) * 2 < lim;
+  if (!(M >= 1 && M <= kSkinnyMaxM && K % kPiece == 0 && N >= 1 && N * K * bits / 8 < lim &&
+        M * K * 2 < lim && N * (K / gs) * 2 < lim))
+    return false;
+  return skinny_lds(plan_skinny((int)N, (int)K, bits, gs), K, gs) <= kSkMaxLds;
 }
 
 hipError_t launch_skinny(const QmvArgs& a) {
