@@ -23,7 +23,7 @@ struct QmvArgs {
 
 // Small batches (M <= kSkinnyMaxM, K % 128 == 0): weights streamed once,
 // M rows on the matrix cores, exact products (kh_skinny.hip).
-constexpr int kSkinnyMaxM = 16;
+constexpr int kSkinnyMaxM = 32;
 bool skinny_supported(int64_t M, int64_t N, int64_t K, int bits, int gs);
 hipError_t launch_skinny(const QmvArgs& a);
 

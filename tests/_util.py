@@ -48,11 +48,24 @@ def gemv_max_m(K: int, bits: int) -> int:
     return 8 if I == 1 else 2 if I == 2 else 1 if I <= 4 else 0
 
 
-def decode_regime(M: int, K: int, bits: int):
+def skinny_fits(M: int, N: int, K: int) -> bool:
+    """The skinny MFMA kernel's own range rule (kh_skinny.hip): K % 128 == 0,
+    5 <= M <= 32, and above 16 rows only where ceil(N/16) * W waves fit one
+    round (W = the largest divisor of K/128 up to 8)."""
+    if K % 128 or not 5 <= M <= 32:
+        return False
+    if M <= 16:
+        return True
+    np_ = K // 128
+    W = max(w for w in range(1, 9) if np_ % w == 0)
+    return -(-N // 16) * W <= 3 * 4 * 256
+
+
+def decode_regime(M: int, K: int, bits: int, N: int):
     """Which kernel (and tiling class) kh_quantized_matmul uses for a
     transpose=true call with bf16/f16 x and 16-bit scales: rows of the result
     are bitwise identical for every M of one regime (kiln_hip.hip, run_qmm)."""
-    if 5 <= M <= 16 and K % 128 == 0:
+    if skinny_fits(M, N, K):
         return ("skinny",)
     if M <= gemv_max_m(K, bits):
         return ("gemv",)
@@ -64,9 +77,9 @@ def decode_regime(M: int, K: int, bits: int):
     return ("qmv",) if M <= 16 else ("qmm", -(-M // 256))
 
 
-def exact_weights(M: int, K: int, bits: int) -> bool:
+def exact_weights(M: int, K: int, bits: int, N: int) -> bool:
     """True where every dequantised weight enters the products unrounded
     (the decode GEMV, the skinny MFMA kernel and qmv); the GEMM kernels round
     each weight once to fp16."""
-    r = decode_regime(M, K, bits)[0]
+    r = decode_regime(M, K, bits, N)[0]
     return r in ("gemv", "skinny", "qmv")

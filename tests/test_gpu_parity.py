@@ -50,13 +50,14 @@ def _run(L, x, gs, bits, xdt, sdt, odt, transpose=True):
 EXACT_REL, F16W_REL = 3e-5, 2.0 ** -11 + 3e-5
 
 
-def rel_for(M, K, bits, transpose=True):
-    return EXACT_REL if (not transpose or exact_weights(M, K, bits)) else F16W_REL
+def rel_for(M, K, bits, transpose=True, N=1):
+    return EXACT_REL if (not transpose or exact_weights(M, K, bits, N)) else F16W_REL
 
 
 def _check_f32(oracle, L, x, gs, bits, xdt, sdt, y, transpose=True, rel=None):
     if rel is None:
-        rel = rel_for(x.reshape(-1, x.shape[-1]).shape[0], x.shape[-1], bits, transpose)
+        N = L["w"].shape[0] if transpose else L["w"].shape[1] * (32 // bits)
+        rel = rel_for(x.reshape(-1, x.shape[-1]).shape[0], x.shape[-1], bits, transpose, N)
     ref = oracle.quantized_matmul_f32(x, xdt, L["w"], L["scales"], L["biases"], sdt, gs, bits, transpose)
     W = oracle.to_f32(oracle.dequantize(L["w"], L["scales"], L["biases"], sdt, gs, bits, "f32"), "f32")
     mag = np.abs(oracle.to_f32(x, xdt)).astype(np.float64) @ np.abs(W.T if transpose else W).astype(np.float64)
@@ -135,7 +136,7 @@ def test_rows_are_m_invariant(bits, gs, K):
     L, x = _case(200, N, K, gs, bits, seed=21)
     groups = {}
     for M in (1, 2, 3, 4, 5, 6, 15, 16, 17, 20, 31, 32, 33, 64, 65, 100, 128, 129, 200):
-        groups.setdefault(decode_regime(M, K, bits), []).append(M)
+        groups.setdefault(decode_regime(M, K, bits, N), []).append(M)
     for regime, Ms in groups.items():
         big = _run(L, x[:max(Ms)], gs, bits, "bf16", "f16", "bf16")
         for M in Ms[:-1]:

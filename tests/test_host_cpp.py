@@ -122,7 +122,7 @@ def test_linear_embedding_head_from_checkpoint(oracle, tmp_path, sharded):
     rc, out, err = _job(tmp_path, model_dir=str(d), op="probe", prefix="model.embed_tokens", k=256,
                         input=str(tmp_path / "b.bin"), input_shape=[1, 1, 64], input_dtype="float16")
     assert rc == 0 and out["ok"], (out, err)
-    first = next(m for m in range(2, 300) if decode_regime(m, 256, 4) != decode_regime(1, 256, 4))
+    first = next(m for m in range(2, 300) if decode_regime(m, 256, 4, 200) != decode_regime(1, 256, 4, 200))
     assert out["m"] == first
 
 
