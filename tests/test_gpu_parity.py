@@ -564,3 +564,20 @@ def test_quantize_unaligned_input(oracle):
     view.copy_(dev(w, "bf16"))
     for g, x in zip(ops.quantize(view, gs, bits), oracle.quantize(w, "bf16", gs, bits)):
         assert np.array_equal(host(g), x)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (4, 128), (8, 32), (8, 64), (8, 128)])
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
+def test_skinny_kernel_exact(oracle, bits, gs, xdt):
+    """The small-batch MFMA kernel (5 <= M <= 32, K % 128 == 0) keeps every
+    dequantised weight exact: ragged N, one piece (K = 128, one wave), odd
+    piece counts per wave (K = 896), one and two m-tiles, the 8-bit bf16
+    nibble-split operands."""
+    for N, K in ((37, 128), (272, 896), (50, 4096)):
+        for M in (5, 13, 16, 17, 32):
+            print(f"case skinny bits={bits} gs={gs} xdt={xdt} N={N} K={K} M={M}", flush=True)
+            assert decode_regime(M, K, bits, N)[0] == "skinny"
+            L, x = _case(M, N, K, gs, bits, xdt=xdt, seed=M + N + K + bits)
+            y = _run(L, x, gs, bits, xdt, "f16", "f32")
+            _check_f32(oracle, L, x, gs, bits, xdt, "f16", y, rel=EXACT_REL)
