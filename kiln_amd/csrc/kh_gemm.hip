@@ -16,7 +16,8 @@
 // stages of 128 codes:
 //   - codes go from HBM straight into registers in MFMA operand layout
 //     (lane (n, lg) holds 16 bytes of row n: one load per 16-row tile at 4
-//     bits, two at 8 bits), prefetched two stages ahead;
+//     bits, two at 8 bits), prefetched three stages ahead, cached normally
+//     (every row tile of the launch re-reads them);
 //   - the activation tile of the stage (16*MT rows x 128 k, float16) is
 //     copied HBM/L2 -> LDS by the direct global-to-LDS loads of gfx950 (each
 //     instruction four whole rows, 1 KB contiguous), into a ring of LDS
@@ -123,7 +124,8 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 // smallest tiles (latency-bound launches) and the largest (one wave per SIMD:
 // the ring is what hides memory latency), 2 at 64 rows.
 #ifndef KH_GEMM_NT
-#define KH_GEMM_NT 1  // code loads marked non-temporal
+#define KH_GEMM_NT 0  // code loads marked non-temporal (measured: 3-7% slower: the codes of
+                      // a column tile are re-read by every row tile and now stay cached)
 #endif
 #ifndef KH_GEMM_CAP
 #define KH_GEMM_CAP 256  // split-K target: workgroups per launch (one per CU)
