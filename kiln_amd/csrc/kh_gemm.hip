@@ -26,8 +26,9 @@
 //   - one barrier per stage.
 // K slices (split-K, chosen from N, K and M-tiles only) write float32
 // partials that gemm_reduce sums in slice order, so results are
-// deterministic. Tiles are ordered so that the workgroups resident on one
-// XCD share the activation panel in that XCD's L2.
+// deterministic. Tiles are ordered in bands of 4 m-tiles (m fastest within a
+// band) and dealt to XCDs in consecutive runs, so the workgroups resident on
+// one XCD share both the activation panels and the code rows in its L2.
 #include "kh_common.h"
 #include "kh_kernels.h"
 
@@ -127,6 +128,9 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 #define KH_GEMM_NT 0  // code loads marked non-temporal (measured: 3-7% slower: the codes of
                       // a column tile are re-read by every row tile and now stay cached)
 #endif
+#ifndef KH_GEMM_GM
+#define KH_GEMM_GM 4  // m-tiles per band of the tile order (1 = n fastest; 4 measured best)
+#endif
 #ifndef KH_GEMM_CAP
 #define KH_GEMM_CAP 256  // split-K target: workgroups per launch (one per CU)
 #endif
@@ -197,8 +201,17 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   const int u0 = t % (cnt * SUB);
   const int sp = t / (cnt * SUB);
   const int tile = tile0 + u0 / SUB;
-  const int tn = tile % tiles_n;
-  const int tm = tile / tiles_n;
+  int tn = tile % tiles_n, tm = tile / tiles_n;
+  if (KH_GEMM_GM > 1) {
+    // bands of GM m-tiles, m fastest within a band: the workgroups resident
+    // on one XCD at a time share both activation panels and code rows in L2
+    const int tiles_m = (M + BM - 1) / BM;
+    const int b0 = (tile / (KH_GEMM_GM * tiles_n)) * KH_GEMM_GM;
+    const int bh = min(KH_GEMM_GM, tiles_m - b0);
+    const int rr = tile - b0 * tiles_n;
+    tm = b0 + rr % bh;
+    tn = rr / bh;
+  }
 
   const int m0 = tm * BM, n0 = tn * kBN + (u0 % SUB) * BN;
   const int k0 = sp * kslice;
