@@ -138,10 +138,10 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 #define KH_GEMM_TAIL 1  // run a partial last round of 128-row tiles as half-width workgroups
 #endif
 #ifndef KH_GEMM_P
-#define KH_GEMM_P 0   // tuning: force the ring depth (0 = by tile size)
+#define KH_GEMM_P 0   // tuning: force the ring depth of 128-row tiles (0 = by tile size)
 #endif
 constexpr int ring_depth(int bits, int mt) {
-  return KH_GEMM_P ? KH_GEMM_P : (mt == 4 ? 2 : 4);
+  return KH_GEMM_P && mt == 8 ? KH_GEMM_P : (mt == 4 ? 2 : 4);
 }
 
 // Scale/bias chunk: the groups of P stages (P*128 codes) of every row of the
@@ -406,7 +406,8 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   // blocks XOR-swizzled by row so the scattered writes spread over the banks.
   // Tiles taller than the ring holds go in passes of EP m-tiles.
   constexpr int RING_BYTES = P * SLOTS * 16;
-  constexpr int EP = RING_BYTES / (16 * BN * 4) < MT ? RING_BYTES / (16 * BN * 4) : MT;
+  constexpr int EP_CAP = RING_BYTES / (16 * BN * 4) < MT ? RING_BYTES / (16 * BN * 4) : MT;
+  constexpr int EP = EP_CAP >= 8 ? 8 : EP_CAP >= 4 ? 4 : EP_CAP >= 2 ? 2 : 1;  // divides MT
   static_assert(EP >= 1 && MT % EP == 0, "epilogue passes");
   float* T = reinterpret_cast<float*>(&As[0][0]);
   auto tidx = [](int r, int c) {  // float index of (row r, column c) in T
