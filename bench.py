@@ -340,6 +340,33 @@ def run_sweep(torch, ops, l8_layers, l8_shapes, graph_us, layer_fns, layer_copie
     qb = Nq * Kq * 2 + Nq * Kq // 2 + 2 * Nq * (Kq // 64) * 2
     out["quantize-14336x4096-bf16-q4-gs64"] = {"us": round(us, 2), "gbs": round(qb / (us * 1e-6) / 1e9, 1)}
     del wsrc, qo
+
+    # MoE expert dispatch (gather_qmm) as SwitchGlu issues it (moe.rs:272-310):
+    # OLMoE experts (E=64, top-8, hidden 2048, intermediate 1024), 4-bit gs64,
+    # T tokens -> T*8 one-row pairs sorted by expert; gate/up shape and down.
+    E, k = 64, 8
+    for name, Ne, Ke in (("gate", 1024, 2048), ("down", 2048, 1024)):
+        Ls = [make_linear_device(Ne, Ke, 64, "q4", seed=e) for e in range(E)]
+        we = torch.stack([L["w"] for L in Ls])
+        se = torch.stack([L["scales"] for L in Ls])
+        be = torch.stack([L["biases"] for L in Ls])
+        del Ls
+        for T in (8, 128, 2048):
+            g = torch.Generator(device=dev)
+            g.manual_seed(T)
+            ids = torch.stack([torch.randperm(E, device=dev, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+            order = torch.argsort(ids.reshape(-1), stable=True)
+            xt = torch.randn((T, Ke), device=dev, generator=g).bfloat16()
+            xg = xt[order // k].reshape(T * k, 1, Ke).contiguous()
+            idx = ids.reshape(-1)[order].contiguous()
+            ye = torch.empty((T * k, 1, Ne), dtype=torch.bfloat16, device=dev)
+            us = graph_us(lambda c: ops.gather_qmm(xg, we, se, be, idx, True, 64, 4, True, out=ye), 1, 20)
+            touched = int(torch.unique(idx).numel())
+            gb = touched * call_bytes(Ne, Ke, 0, 4, 64) + T * k * (Ke + Ne) * 2
+            out[f"olmoe-gather_qmm-{name}-{Ne}x{Ke}-T{T}"] = {
+                "us": round(us, 2), "tflops": round(2 * T * k * Ne * Ke / (us * 1e-6) / 1e12, 2),
+                "gbs": round(gb / (us * 1e-6) / 1e9, 1), "experts_touched": touched}
+        del we, se, be
     return out
 
 

@@ -187,9 +187,13 @@ int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gat
  * scales/biases [E, N, K/gs]; rhs_indices uint32|int32; res [batch..., M, N].
  * transpose must be true (Kiln's only use). Negative int32 ids count from
  * the end; ids outside [-E, E) give zero rows. sorted_indices is the
- * reference's scheduling hint and does not change results. Numerics per
- * pair as kh_quantized_matmul's decode path (exact products) where it
- * applies, else an exact float32 chain. */
+ * reference's scheduling hint and does not change results. Small batches
+ * run pair by pair with kh_quantized_matmul's decode numerics (exact
+ * products). From 64 rows (pairs x M) and 2 rows per possible expert on
+ * average, and for every M above the decode range, the rows are grouped by
+ * expert on the device and run as one MFMA GEMM: each row then equals
+ * kh_quantized_matmul's GEMM path on that row (float16 weights). float32 x
+ * or scales take an exact float32 chain. */
 int kh_gather_qmm(kh_array* res, const kh_array* x, const kh_array* w, const kh_array* scales,
                   const kh_array* biases, const kh_array* rhs_indices, bool transpose,
                   kh_optional_int group_size, kh_optional_int bits, const char* mode,

@@ -166,12 +166,17 @@ struct ScaleChunk {
   static constexpr int OPS = 2 * BN * PIECES / (64 * kWaves);  // direct loads per lane
 };
 
-template <int BITS, bool SF16, int MT, int GS, int NT>
+// GR (grouped, gather_qmm): x holds the rows of every expert group, each
+// group padded to whole m-tiles; gtab[0] is the number of m-tiles in use and
+// gtab[1 + tm] the expert of m-tile tm (w, scales and biases are [E, N, ..]
+// stacks); rowmap[m] is the output row of padded row m, or -1 for padding.
+template <int BITS, bool SF16, int MT, int GS, int NT, bool GR>
 __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     const u32x4* __restrict__ xh, const float* __restrict__ rscale,
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, float* __restrict__ part, void* __restrict__ out,
-    int odt, int M, int N, int K, int kslice, int tiles_n, int tile0, int cnt, int nsplit) {
+    int odt, int M, int N, int K, int kslice, int tiles_n, int tile0, int cnt, int nsplit,
+    const int* __restrict__ gtab, const int* __restrict__ rowmap) {
   // NT 16-column MFMA tiles per wave: 4 (a 256-column tile) or 2 (half of
   // one, for the last partial round of a launch)
   constexpr int BN = kWaves * NT * 16;
@@ -194,8 +199,12 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   // XCD-aware tile order: workgroup b runs on XCD b % 8; the work items of
   // one XCD are consecutive in (split, tile, part of tile) order, with tiles
   // tile0 .. tile0+cnt-1 numbered m-tile-major, n fastest.
-  const int total = cnt * SUB * nsplit;
+  // Grouped: only the m-tiles in use (a device-side count) are dealt out, so
+  // they spread over all XCDs; the grid was sized for the most there can be.
+  const int tiles_m = GR ? gtab[0] : (M + BM - 1) / BM;
+  const int total = GR ? tiles_m * tiles_n * SUB : cnt * SUB * nsplit;
   const int per = (total + kXcds - 1) / kXcds;
+  if (GR && (int)blockIdx.x / kXcds >= per) return;
   const int t = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
   if (t >= total) return;
   const int u0 = t % (cnt * SUB);
@@ -205,7 +214,6 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   if (KH_GEMM_GM > 1) {
     // bands of GM m-tiles, m fastest within a band: the workgroups resident
     // on one XCD at a time share both activation panels and code rows in L2
-    const int tiles_m = (M + BM - 1) / BM;
     const int b0 = (tile / (KH_GEMM_GM * tiles_n)) * KH_GEMM_GM;
     const int bh = min(KH_GEMM_GM, tiles_m - b0);
     const int rr = tile - b0 * tiles_n;
@@ -213,6 +221,12 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     tn = rr / bh;
   }
 
+  if constexpr (GR) {
+    const int64_t e = gtab[1 + tm];
+    w += e * N * (K * BITS / 32);
+    scales += e * N * (K >> LGS);
+    biases += e * N * (K >> LGS);
+  }
   const int m0 = tm * BM, n0 = tn * kBN + (u0 % SUB) * BN;
   const int k0 = sp * kslice;
   const int k1 = min(K, k0 + kslice);
@@ -434,8 +448,13 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
 #pragma unroll
     for (int b0 = 0; b0 < BLOCKS; b0 += 64 * kWaves) {
       const int b = b0 + tid, r = b / (BN / 4), c = (b % (BN / 4)) * 4;
-      const int m = m0 + i0 * 16 + r, n = n0 + c;
+      int m = m0 + i0 * 16 + r;
+      const int n = n0 + c;
       if (m >= M || n >= N) continue;
+      if constexpr (GR) {
+        m = rowmap[m];  // output row (split-K is never used here)
+        if (m < 0) continue;
+      }
       const f32x4 v = *reinterpret_cast<const f32x4*>(&T[tidx(r, c)]);
       if (nsplit > 1) {
         float* dst = part + ((int64_t)sp * M + m) * N + n;
@@ -506,48 +525,55 @@ size_t gemm_partial_bytes(const GemmPlan& p, int M, int N) {
 
 bool gemm_supported(int K) { return K % kStage == 0; }
 
-template <int BITS, bool SF16, int MT, int GS, int NT>
+template <int BITS, bool SF16, int MT, int GS, int NT, bool GR>
 static hipError_t launch_range(const QmvArgs& a, const GemmPlan& p, const u32x4* xh,
-                               const float* rsc, float* part, int tile0, int cnt, int nsplit) {
+                               const float* rsc, float* part, int tile0, int cnt, int nsplit,
+                               const int* gtab, const int* rowmap) {
   const int total = cnt * (4 / NT) * nsplit;
   const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
-  hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS, NT>), dim3(grid), dim3(64 * kWaves), 0,
+  hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS, NT, GR>), dim3(grid), dim3(64 * kWaves), 0,
                      a.stream, xh, rsc, (const uint32_t*)a.w, (const uint16_t*)a.scales,
                      (const uint16_t*)a.biases, part, a.out, a.odt, a.M, a.N, a.K, p.kslice,
-                     p.tiles_n, tile0, cnt, nsplit);
+                     p.tiles_n, tile0, cnt, nsplit, gtab, rowmap);
   return hipGetLastError();
 }
 
-template <int BITS, bool SF16, int MT, int GS>
+template <int BITS, bool SF16, int MT, int GS, bool GR>
 static hipError_t launch_mt(const QmvArgs& a, const GemmPlan& p, const u32x4* xh, const float* rsc,
-                            float* part) {
+                            float* part, const int* gtab, const int* rowmap) {
   const int T = p.tiles_n * p.tiles_m;
-  hipError_t e = launch_range<BITS, SF16, MT, GS, 4>(a, p, xh, rsc, part, 0, T - p.tail, p.nsplit);
-  if constexpr (MT == kMaxMT) {
-    if (e == hipSuccess && p.tail > 0)
-      e = launch_range<BITS, SF16, MT, GS, 2>(a, p, xh, rsc, part, T - p.tail, p.tail, 1);
+  if constexpr (GR) {
+    return launch_range<BITS, SF16, MT, GS, 4, true>(a, p, xh, rsc, part, 0, T, 1, gtab, rowmap);
+  } else {
+    hipError_t e =
+        launch_range<BITS, SF16, MT, GS, 4, false>(a, p, xh, rsc, part, 0, T - p.tail, p.nsplit, nullptr, nullptr);
+    if constexpr (MT == kMaxMT) {
+      if (e == hipSuccess && p.tail > 0)
+        e = launch_range<BITS, SF16, MT, GS, 2, false>(a, p, xh, rsc, part, T - p.tail, p.tail, 1, nullptr,
+                                                       nullptr);
+    }
+    return e;
   }
-  return e;
 }
 
-template <int BITS, bool SF16, int GS>
+template <int BITS, bool SF16, int GS, bool GR>
 static hipError_t launch_g(const QmvArgs& a, const GemmPlan& p, const u32x4* xh, const float* rsc,
-                           float* part) {
+                           float* part, const int* gtab, const int* rowmap) {
   switch (p.mt) {
-    case 1: return launch_mt<BITS, SF16, 1, GS>(a, p, xh, rsc, part);
-    case 2: return launch_mt<BITS, SF16, 2, GS>(a, p, xh, rsc, part);
-    case 4: return launch_mt<BITS, SF16, 4, GS>(a, p, xh, rsc, part);
-    default: return launch_mt<BITS, SF16, 8, GS>(a, p, xh, rsc, part);
+    case 1: return launch_mt<BITS, SF16, 1, GS, GR>(a, p, xh, rsc, part, gtab, rowmap);
+    case 2: return launch_mt<BITS, SF16, 2, GS, GR>(a, p, xh, rsc, part, gtab, rowmap);
+    case 4: return launch_mt<BITS, SF16, 4, GS, GR>(a, p, xh, rsc, part, gtab, rowmap);
+    default: return launch_mt<BITS, SF16, 8, GS, GR>(a, p, xh, rsc, part, gtab, rowmap);
   }
 }
 
-template <int BITS, bool SF16>
+template <int BITS, bool SF16, bool GR>
 static hipError_t launch_s(const QmvArgs& a, const GemmPlan& p, const u32x4* xh, const float* rsc,
-                           float* part) {
+                           float* part, const int* gtab = nullptr, const int* rowmap = nullptr) {
   switch (a.gs) {
-    case 32: return launch_g<BITS, SF16, 32>(a, p, xh, rsc, part);
-    case 64: return launch_g<BITS, SF16, 64>(a, p, xh, rsc, part);
-    default: return launch_g<BITS, SF16, 128>(a, p, xh, rsc, part);
+    case 32: return launch_g<BITS, SF16, 32, GR>(a, p, xh, rsc, part, gtab, rowmap);
+    case 64: return launch_g<BITS, SF16, 64, GR>(a, p, xh, rsc, part, gtab, rowmap);
+    default: return launch_g<BITS, SF16, 128, GR>(a, p, xh, rsc, part, gtab, rowmap);
   }
 }
 
@@ -558,14 +584,34 @@ hipError_t launch_gemm(const QmvArgs& a, const GemmPlan& p, const void* xh, cons
   const u32x4* x4 = static_cast<const u32x4*>(xh);
   const bool sf16 = a.sdt == DT_F16;
   if (a.bits == 4)
-    e = sf16 ? launch_s<4, true>(a, p, x4, rsc, part) : launch_s<4, false>(a, p, x4, rsc, part);
+    e = sf16 ? launch_s<4, true, false>(a, p, x4, rsc, part) : launch_s<4, false, false>(a, p, x4, rsc, part);
   else
-    e = sf16 ? launch_s<8, true>(a, p, x4, rsc, part) : launch_s<8, false>(a, p, x4, rsc, part);
+    e = sf16 ? launch_s<8, true, false>(a, p, x4, rsc, part) : launch_s<8, false, false>(a, p, x4, rsc, part);
   if (e != hipSuccess || p.nsplit == 1) return e;
   const int64_t MN = (int64_t)a.M * a.N;
   hipLaunchKernelGGL(gemm_reduce, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, a.stream, part,
                      a.out, a.odt, MN, p.nsplit);
   return hipGetLastError();
+}
+
+// Grouped GEMM over expert stacks: a.M is the padded row count
+// (tiles_max * 16 * mt), a.out has the real rows; see gemm_kernel's GR mode.
+hipError_t launch_gemm_grouped(const QmvArgs& a, int mt, int tiles_max, const void* xh,
+                               const float* rsc, const int* gtab, const int* rowmap) {
+  GemmPlan p;
+  p.mt = mt;
+  p.tiles_m = tiles_max;
+  p.tiles_n = (a.N + kBN - 1) / kBN;
+  p.nsplit = 1;
+  p.kslice = a.K;
+  p.tail = 0;
+  const u32x4* x4 = static_cast<const u32x4*>(xh);
+  const bool sf16 = a.sdt == DT_F16;
+  if (a.bits == 4)
+    return sf16 ? launch_s<4, true, true>(a, p, x4, rsc, nullptr, gtab, rowmap)
+                : launch_s<4, false, true>(a, p, x4, rsc, nullptr, gtab, rowmap);
+  return sf16 ? launch_s<8, true, true>(a, p, x4, rsc, nullptr, gtab, rowmap)
+              : launch_s<8, false, true>(a, p, x4, rsc, nullptr, gtab, rowmap);
 }
 
 }  // namespace kh

@@ -54,6 +54,22 @@ struct GatherArgs {
   int shape[8];
   int64_t xs[8], is[8];
 };
+// Expert of pair b (g.E when the id is outside [-E, E)); *xo = the pair's
+// element offset into x.
+__device__ __forceinline__ int gather_expert(const GatherArgs& g, int64_t b, int64_t* xo) {
+  int64_t xoff = 0, io = 0, rem = b;
+  for (int d = g.nd - 1; d >= 0; --d) {
+    const int64_t c = rem % g.shape[d];
+    rem /= g.shape[d];
+    xoff += c * g.xs[d];
+    io += c * g.is[d];
+  }
+  int64_t e = g.idx_signed ? (int64_t) static_cast<const int32_t*>(g.idx)[io]
+                           : (int64_t) static_cast<const uint32_t*>(g.idx)[io];
+  if (e < 0) e += g.E;
+  *xo = xoff;
+  return e >= 0 && e < g.E ? (int)e : g.E;
+}
 hipError_t launch_gemv_gather(const QmvArgs& a, const GatherArgs& g);
 // Any dtype/alignment/M: one thread per output, float32 fma chain.
 hipError_t launch_gather_generic(const QmvArgs& a, const GatherArgs& g);
@@ -78,6 +94,25 @@ size_t qmm_workspace_bytes(int M, int K);
 // x -> float16 rows scaled by an exact power of two (rsc[m] = 2^e_m), in the
 // pair order of the code operands: xh holds M*K*2 bytes, 16-byte aligned.
 hipError_t launch_prep_x(const QmvArgs& a, void* xh, float* rsc);
+
+// gather_qmm at prefill sizes (kh_group.hip): the batch's rows grouped by
+// expert, each group padded to whole m-tiles of 16*mt rows, through the
+// GEMM in grouped mode. Experts 0..kGroupMaxE-1 (ids beyond give zero rows).
+constexpr int kGroupMaxE = 1023;
+struct GroupPlan {
+  int mt;
+  int64_t rows;       // pairs * M
+  int64_t tiles_max;  // m-tiles the padded buffer holds
+  int64_t padded;     // tiles_max * 16 * mt
+};
+GroupPlan plan_group(const QmvArgs& a, const GatherArgs& g);
+// Workspace bytes of the grouped call (16-byte aligned pieces).
+size_t group_workspace_bytes(const GroupPlan& p, const QmvArgs& a, const GatherArgs& g);
+hipError_t launch_gather_grouped(const QmvArgs& a, const GatherArgs& g, const GroupPlan& p, void* ws);
+hipError_t launch_group_prep_x(const QmvArgs& a, const GatherArgs& g, const int* pos, void* xh,
+                               float* rsc, int* rowmap);
+hipError_t launch_gemm_grouped(const QmvArgs& a, int mt, int tiles_max, const void* xh,
+                               const float* rsc, const int* gtab, const int* rowmap);
 
 // Quantized GEMM for every M above the VALU-GEMV range (K % 128 == 0): a
 // (16*mt) x 256 tile per workgroup, float16 MFMA on weights dequantised once

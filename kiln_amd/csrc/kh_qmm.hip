@@ -63,17 +63,20 @@ __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
 
 }  // namespace
 
-// xh[m] = permuted float16 of x[m] * 2^-e_m, rscale[m] = 2^e_m, with e_m >= 0
-// the smallest exponent keeping max|x[m]| * 2^-e_m below 2^15. One
-// workgroup per row.
+// dst = permuted float16 of row * 2^-e, *rs = 2^e, with e >= 0 the smallest
+// exponent keeping max|row| * 2^-e below 2^15. Called by all 256 threads of a
+// workgroup (red: 256 floats of LDS). zero: write a zero row and *rs = 0.
 template <int BITS, bool XBF16>
-__global__ __launch_bounds__(256) void qmm_prep_x(const uint16_t* __restrict__ x,
-                                                  u32x4* __restrict__ xh,
-                                                  float* __restrict__ rscale, int K) {
-  __shared__ float red[256];
-  const int m = blockIdx.x, tid = threadIdx.x;
-  const u32x4* row = reinterpret_cast<const u32x4*>(x + (int64_t)m * K);
+__device__ __forceinline__ void prep_row(const uint16_t* __restrict__ x, u32x4* __restrict__ dst,
+                                         float* __restrict__ rs, int K, bool zero, float* red) {
+  const int tid = threadIdx.x;
+  const u32x4* row = reinterpret_cast<const u32x4*>(x);
   const int nb = K / 8;
+  if (zero) {
+    for (int c = tid; c < nb; c += 256) dst[c] = u32x4{0u, 0u, 0u, 0u};
+    if (tid == 0) *rs = 0.f;
+    return;
+  }
   float mx = 0.f;
   for (int c = tid; c < nb; c += 256) {
     const u32x4 v = row[c];
@@ -98,8 +101,7 @@ __global__ __launch_bounds__(256) void qmm_prep_x(const uint16_t* __restrict__ x
     ex = e2 - 15;           // mx * 2^-ex < 2^15
   }
   const float inv = ldexpf(1.f, -ex);
-  if (tid == 0) rscale[m] = ldexpf(1.f, ex);
-  u32x4* dst = xh + (int64_t)m * nb;
+  if (tid == 0) *rs = ldexpf(1.f, ex);
   for (int c = tid; c < nb; c += 256) {
     const u32x4 v = row[c];
     u32x4 o;
@@ -110,6 +112,37 @@ __global__ __launch_bounds__(256) void qmm_prep_x(const uint16_t* __restrict__ x
       o[e] = f32_to_f16_bits(lo * inv) | (f32_to_f16_bits(hi * inv) << 16);
     }
     dst[c] = permute_x<BITS>(o);
+  }
+}
+
+// xh[m], rscale[m] = prep_row(x[m]). One workgroup per row.
+template <int BITS, bool XBF16>
+__global__ __launch_bounds__(256) void qmm_prep_x(const uint16_t* __restrict__ x,
+                                                  u32x4* __restrict__ xh,
+                                                  float* __restrict__ rscale, int K) {
+  __shared__ float red[256];
+  const int m = blockIdx.x;
+  prep_row<BITS, XBF16>(x + (int64_t)m * K, xh + (int64_t)m * (K / 8), rscale + m, K, false, red);
+}
+
+// Grouped (gather_qmm) rows: row r = pair b * M + i of the batch goes to
+// padded row pos[b] + i; rowmap records r there. Pairs whose expert id is
+// out of range get a zero row and scale 0 (their outputs are zeros).
+template <int BITS, bool XBF16>
+__global__ __launch_bounds__(256) void group_prep_x(const uint16_t* __restrict__ x, GatherArgs g, int M,
+                                                    const int* __restrict__ pos, u32x4* __restrict__ xh,
+                                                    float* __restrict__ rscale, int* __restrict__ rowmap,
+                                                    int K) {
+  __shared__ float red[256];
+  for (int64_t r = blockIdx.x; r < g.pairs * M; r += gridDim.x) {
+    const int64_t b = r / M;
+    const int i = (int)(r % M);
+    int64_t xo;
+    const int e = gather_expert(g, b, &xo);
+    const int64_t pr = pos[b] + i;
+    prep_row<BITS, XBF16>(x + xo + (int64_t)i * K, xh + pr * (K / 8), rscale + pr, K, e >= g.E, red);
+    if (threadIdx.x == 0) rowmap[pr] = (int)r;
+    __syncthreads();  // red is reused by the next row
   }
 }
 
@@ -318,6 +351,24 @@ static hipError_t launch_gs(const QmvArgs& a, const u32x4* xh, const float* rsc)
 
 // `ws` holds qmm_workspace_bytes(M, K) bytes (16-byte aligned). Scales and
 // biases are float16 or bfloat16.
+hipError_t launch_group_prep_x(const QmvArgs& a, const GatherArgs& g, const int* pos, void* xh_,
+                               float* rsc, int* rowmap) {
+  u32x4* xh = static_cast<u32x4*>(xh_);
+  const bool xbf16 = a.xdt == DT_BF16;
+  const int64_t rows = g.pairs * a.M;
+  const unsigned grid = (unsigned)(rows < (1 << 20) ? rows : (1 << 20));
+#define KH_GPREP(B, X)                                                                              \
+  hipLaunchKernelGGL((group_prep_x<B, X>), dim3(grid), dim3(256), 0, a.stream, (const uint16_t*)a.x, g, \
+                     a.M, pos, xh, rsc, rowmap, a.K)
+  if (a.bits == 4) {
+    if (xbf16) KH_GPREP(4, true); else KH_GPREP(4, false);
+  } else {
+    if (xbf16) KH_GPREP(8, true); else KH_GPREP(8, false);
+  }
+#undef KH_GPREP
+  return hipGetLastError();
+}
+
 hipError_t launch_prep_x(const QmvArgs& a, void* xh_, float* rsc) {
   u32x4* xh = static_cast<u32x4*>(xh_);
   const bool xbf16 = a.xdt == DT_BF16;

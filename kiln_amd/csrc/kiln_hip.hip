@@ -8,6 +8,7 @@
 // call, so validation behaves identically on a machine without a GPU.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -323,6 +324,12 @@ bool fast_path(const kh::QmvArgs& a, bool transpose) {
 bool skinny_path(const kh::QmvArgs& a) {
   return a.M >= KH_SKINNY_MIN_M && kh::skinny_supported(a.M, a.N, a.K, a.bits, a.gs);
 }
+#ifndef KH_GROUP_MIN_ROWS
+#define KH_GROUP_MIN_ROWS 64  // gather_qmm: fewest rows (pairs * M) for the grouped GEMM
+#endif
+#ifndef KH_GROUP_MIN_AVG
+#define KH_GROUP_MIN_AVG 2    // ... and fewest rows per possible expert group
+#endif
 bool gemv_path(const kh::QmvArgs& a) {
   return a.M <= kh::gemv_max_m(a.K, a.bits) && kh::gemv_fits(a.M, a.N, a.K, a.bits, a.gs);
 }
@@ -523,10 +530,27 @@ int kh_gather_qmm(kh_array* res, const kh_array* x, const kh_array* w, const kh_
   kh::QmvArgs a{x->data, x->dtype, w->data, scales->data, biases->data, scales->dtype, res->data,
                 res->dtype, (int)M, (int)N, (int)K, gs, bits, static_cast<hipStream_t>(stream)};
   hipError_t e;
-  if (fast_path(a, true) && gemv_path(a) && aligned16(x->data))
+  const bool fast = fast_path(a, true);
+  const bool gemv = fast && gemv_path(a);
+  // Grouped GEMM once the expert groups hold a few rows each (a pair-by-pair
+  // GEMV streams the expert's weights once per pair), and for every M the
+  // GEMV does not take.
+  const int64_t groups = std::min<int64_t>(E + 1, pairs), nrows = pairs * M;
+  const bool grouped = fast && kh::gemm_supported((int)K) && E <= kh::kGroupMaxE &&
+                       (!gemv || (nrows >= KH_GROUP_MIN_ROWS && nrows >= KH_GROUP_MIN_AVG * groups));
+  if (grouped) {
+    const kh::GroupPlan gp = kh::plan_group(a, g);
+    if (gp.padded > INT32_MAX)
+      return fail(KH_ERR_UNSUPPORTED, "[%s] %lld rows after grouping exceed 2^31", op, (long long)gp.padded);
+    Workspace ws;
+    const size_t bytes = kh::group_workspace_bytes(gp, a, g);
+    if (!workspace(a.stream, (bytes + 3) / 4, &ws, &rc, op)) return rc;
+    e = kh::launch_gather_grouped(a, g, gp, ws.data);
+  } else if (gemv) {
     e = kh::launch_gemv_gather(a, g);
-  else
+  } else {
     e = kh::launch_gather_generic(a, g);
+  }
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
 }
 

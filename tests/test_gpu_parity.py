@@ -364,8 +364,8 @@ def test_fused_entry_points_validate():
 
 # ----------------------------------------------------------------- gather_qmm (MoE expert dispatch)
 
-def _experts(E, N, K, gs, bits, seed):
-    Ls = [make_linear_numpy(N, K, gs, "q4" if bits == 4 else "q8", seed=seed + e) for e in range(E)]
+def _experts(E, N, K, gs, bits, seed, sdt="f16"):
+    Ls = [make_linear_numpy(N, K, gs, "q4" if bits == 4 else "q8", seed=seed + e, sdt=sdt) for e in range(E)]
     w = np.stack([L["w"] for L in Ls])
     s = np.stack([L["scales"] for L in Ls])
     b = np.stack([L["biases"] for L in Ls])
@@ -423,9 +423,10 @@ def test_gather_qmm_signed_and_out_of_range_ids(oracle):
 
 @pytest.mark.parametrize("M,xdt", [(2, "bf16"), (12, "bf16"), (3, "f32")])
 def test_gather_qmm_rows_per_pair_and_fallback(oracle, M, xdt):
-    """M rows per pair through the decode kernel (M <= 8) or the exact
-    fallback (M > 8, float32 x): per pair, the oracle's bound (float32 x is
-    the oracle's own chain: bit-exact)."""
+    """M rows per pair through the decode kernel (M in the GEMV range), the
+    grouped GEMM (larger M) or the exact fallback (float32 x): per pair, the
+    oracle's bound for that kernel (float32 x is the oracle's own chain:
+    bit-exact)."""
     E, N, K, P = 3, 80, 256, 4
     w, s, b = _experts(E, N, K, 64, 4, seed=80)
     xs = make_x_numpy(P * M, K, seed=81, xdt=xdt).reshape(P, M, K)
@@ -439,7 +440,72 @@ def test_gather_qmm_rows_per_pair_and_fallback(oracle, M, xdt):
         if xdt == "f32":
             assert np.array_equal(y[p].astype(np.float32).view(np.uint32), ref.astype(np.float32).view(np.uint32))
         else:
-            _check_f32(oracle, L, xs[p], 64, 4, xdt, "f16", y[p], rel=EXACT_REL)
+            rel = EXACT_REL if M <= gemv_max_m(K, 4) else F16W_REL
+            _check_f32(oracle, L, xs[p], 64, 4, xdt, "f16", y[p], rel=rel)
+
+
+def _grouped_ids(T, k, E, seed):
+    """[T, k] expert ids, k distinct per token, every expert used >= 33 times."""
+    rng = np.random.default_rng(seed)
+    base = np.arange(T * k).reshape(T, k) % E
+    return ((base + rng.integers(0, E, (T, 1))) % E).astype(np.uint32)
+
+
+@pytest.mark.parametrize("layout", ["sorted", "unsorted"])
+@pytest.mark.parametrize("E,T,k", [(4, 80, 2), (2, 200, 1), (6, 100, 3)])
+@pytest.mark.parametrize("bits,gs,sdt", [(4, 64, "f16"), (8, 32, "bf16"), (4, 128, "bf16")])
+def test_gather_qmm_grouped_gemm(oracle, layout, E, T, k, bits, gs, sdt):
+    """Prefill-size gather_qmm (SwitchGlu's T*k pairs, moe.rs:272-310) runs
+    as one grouped GEMM: every row equals kh_quantized_matmul's GEMM path on
+    its expert's rows bit for bit (K = 512 takes no split-K; a row's result
+    depends neither on its tile nor its neighbours), and the oracle to the
+    float16-weight bound. Tile heights 32, 128 and 64 rows by (E, T, k)."""
+    N, K = 320, 512
+    w, s, b = _experts(E, N, K, gs, bits, seed=100 + E, sdt=sdt)
+    ids = _grouped_ids(T, k, E, seed=101)
+    xs = make_x_numpy(T, K, seed=102, xdt="bf16")
+    if layout == "unsorted":  # x [T,1,1,K] broadcast over the k slots
+        x = dev(xs.reshape(T, 1, 1, K), "bf16")
+        idx = dev(ids)
+        pairs = [(t, j) for t in range(T) for j in range(k)]
+    else:
+        order = np.argsort(ids.reshape(-1), kind="stable")
+        x = dev(xs[order // k].reshape(T * k, 1, K), "bf16")
+        idx = dev(ids.reshape(-1)[order])
+        pairs = [(int(o) // k, int(o) % k) for o in order]
+    y = ops.gather_qmm(x, dev(w), dev(s, sdt), dev(b, sdt), idx, True, gs, bits, layout == "sorted",
+                       out_dtype="f32")
+    torch.cuda.synchronize()
+    yh = host(y).reshape(-1, N)
+    for e in range(E):
+        sel = [p for p, (t, j) in enumerate(pairs) if ids[t, j] == e]
+        toks = [pairs[p][0] for p in sel]
+        assert len(sel) >= 33
+        L = dict(w=w[e], scales=s[e], biases=b[e])
+        ref = host(ops.quantized_matmul(dev(xs[toks], "bf16"), dev(w[e]), dev(s[e], sdt), dev(b[e], sdt),
+                                        True, gs, bits, out_dtype="f32"))
+        assert np.array_equal(yh[sel].view(np.uint32), ref.view(np.uint32)), e
+        _check_f32(oracle, L, xs[toks[:8]], gs, bits, "bf16", sdt, yh[sel[:8]], rel=F16W_REL)
+
+
+def test_gather_qmm_grouped_ids_out_of_range(oracle):
+    """Grouped path with int32 ids: -1 counts from the end, ids outside
+    [-E, E) give zero rows, and the valid rows are unchanged by them."""
+    E, N, K, P = 5, 256, 256, 96
+    w, s, b = _experts(E, N, K, 64, 4, seed=110)
+    xs = make_x_numpy(P, K, seed=111, xdt="bf16")
+    ids = (np.arange(P) % E).astype(np.int32)
+    ids[::7] = -1      # expert 4
+    ids[3::11] = 9     # out of range
+    ids[5::13] = -6    # out of range
+    y = host(ops.gather_qmm(dev(xs.reshape(P, 1, K), "bf16"), dev(w), dev(s, "f16"), dev(b, "f16"),
+                            torch.from_numpy(ids).cuda(), True, 64, 4, out_dtype="f32")).reshape(P, N)
+    bad = (ids >= E) | (ids < -E)
+    assert bad.any() and not y[bad].any()
+    for p in np.flatnonzero(~bad)[:12]:
+        e = int(ids[p]) % E
+        L = dict(w=w[e], scales=s[e], biases=b[e])
+        _check_f32(oracle, L, xs[p:p + 1], 64, 4, "bf16", "f16", y[p:p + 1], rel=F16W_REL)
 
 
 def test_gather_qmm_empty_and_errors():
