@@ -140,13 +140,22 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 #ifndef KH_GEMM_P
 #define KH_GEMM_P 0   // tuning: force the ring depth of 128-row tiles (0 = by tile size)
 #endif
+#ifndef KH_GEMM_WR
+#define KH_GEMM_WR 1  // waves along the rows of 64- and 128-row tiles (2: two waves per SIMD)
+#endif
+// Waves per workgroup along the tile's rows: with 2, eight waves split a
+// tile into 2 row halves x 4 column groups, two per SIMD, so one wave's
+// memory waits overlap the other's MFMAs (each weight is dequantised by both
+// row halves).
+constexpr int wr_for(int mt) { return KH_GEMM_WR == 2 && mt >= 4 ? 2 : 1; }
 constexpr int ring_depth(int bits, int mt) {
-  return KH_GEMM_P && mt == 8 ? KH_GEMM_P : (mt == 4 ? 2 : 4);
+  return KH_GEMM_P && mt == 8 ? KH_GEMM_P
+                              : (wr_for(mt) == 2 ? (bits == 8 ? 2 : 4) : (mt == 4 ? 2 : 4));
 }
 
 // Scale/bias chunk: the groups of P stages (P*128 codes) of every row of the
 // workgroup, copied to LDS by direct loads of SPIECE bytes.
-template <int GS, int P, int BN>
+template <int GS, int P, int BN, int KW>
 struct ScaleChunk {
   static constexpr int GC = P * kStage / GS;            // groups per row
   static constexpr int BYTES = GC * 2;                  // per row and array
@@ -163,7 +172,8 @@ struct ScaleChunk {
   __device__ static constexpr int offset(int arr, int row, int g) {
     return ((arr * BN + row) * PIECES + g / (SPIECE / 2)) * SSTRIDE + (g % (SPIECE / 2)) * 2;
   }
-  static constexpr int OPS = 2 * BN * PIECES / (64 * kWaves);  // direct loads per lane
+  static constexpr int OPS = 2 * BN * PIECES / (64 * KW);  // direct loads per lane
+  static_assert(OPS * 64 * KW == 2 * BN * PIECES, "every wave issues the same loads");
 };
 
 // GR (grouped, gather_qmm): x holds the rows of every expert group, each
@@ -171,7 +181,7 @@ struct ScaleChunk {
 // gtab[1 + tm] the expert of m-tile tm (w, scales and biases are [E, N, ..]
 // stacks); rowmap[m] is the output row of padded row m, or -1 for padding.
 template <int BITS, bool SF16, int MT, int GS, int NT, bool GR>
-__global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
+__global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
     const u32x4* __restrict__ xh, const float* __restrict__ rscale,
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, float* __restrict__ part, void* __restrict__ out,
@@ -179,14 +189,18 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     const int* __restrict__ gtab, const int* __restrict__ rowmap) {
   // NT 16-column MFMA tiles per wave: 4 (a 256-column tile) or 2 (half of
   // one, for the last partial round of a launch)
+  constexpr int WR = wr_for(MT);            // row halves
+  constexpr int KW = kWaves * WR;           // waves per workgroup
+  constexpr int MW = MT / WR;               // 16-row m-tiles per wave
   constexpr int BN = kWaves * NT * 16;
   constexpr int SUB = kBN / BN;           // workgroups per 256-column tile
   constexpr int BM = 16 * MT;
   constexpr int LW = BITS / 4;             // 16-byte code loads per lane per 16-row tile
   constexpr int SLOTS = 16 * BM;           // u32x4 activation slots per stage
-  constexpr int DOPS = (SLOTS + 64 * kWaves - 1) / (64 * kWaves);  // activation loads per lane
+  constexpr int DOPS = (SLOTS + 64 * KW - 1) / (64 * KW);  // activation loads per lane
+  static_assert(WR == 1 || SLOTS % (64 * KW) == 0, "every wave issues the same loads");
   constexpr int P = ring_depth(BITS, MT);  // stages in flight
-  using SC = ScaleChunk<GS, P, BN>;
+  using SC = ScaleChunk<GS, P, BN, KW>;
   constexpr int LGS = __builtin_ctz(GS);
 
   __shared__ u32x4 As[P][SLOTS];
@@ -194,6 +208,8 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  const int wc = WR == 1 ? wave : wave % kWaves;  // column group
+  const int wr = WR == 1 ? 0 : wave / kWaves;     // row half
   const int col = lane & 15, lg = lane >> 4;
 
   // XCD-aware tile order: workgroup b runs on XCD b % 8; the work items of
@@ -240,7 +256,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   int nrow[NT];
 #pragma unroll
   for (int u = 0; u < NT; ++u) {
-    const int n = n0 + wave * (NT * 16) + u * 16 + col;
+    const int n = n0 + wc * (NT * 16) + u * 16 + col;
     nrow[u] = n < N ? n : N - 1;
   }
 
@@ -267,14 +283,14 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     const int kc8 = (k0 + st * kStage) >> 3;
 #pragma unroll
     for (int d = 0; d < DOPS; ++d) {
-      const int s = (d * kWaves + wave) * 64 + lane;
+      const int s = (d * KW + wave) * 64 + lane;
       const int sl = s < SLOTS ? s : SLOTS - 1;
       const int m = sl >> 4, kb = (sl & 15) ^ (m & 15);
       const int mm = m0 + m < M ? m0 + m : M - 1;
-      if ((d * kWaves + wave) * 64 < SLOTS)  // wave-uniform
+      if ((d * KW + wave) * 64 < SLOTS)  // wave-uniform
         __builtin_amdgcn_global_load_lds(
             (const void*)(xh + (int64_t)mm * KB8 + kc8 + kb),
-            (lds_void*)&As[buf][(d * kWaves + wave) * 64], 16, 0, 0);
+            (lds_void*)&As[buf][(d * KW + wave) * 64], 16, 0, 0);
     }
   };
   // Scale/bias chunk c into buffer c & 1: lane op i = (array, row, piece),
@@ -283,7 +299,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     const int g0 = (k0 >> LGS) + c * SC::GC;
 #pragma unroll
     for (int d = 0; d < SC::OPS; ++d) {
-      const int i = (d * kWaves + wave) * 64 + lane;
+      const int i = (d * KW + wave) * 64 + lane;
       const int piece = i % SC::PIECES, row = (i / SC::PIECES) % BN, arr = i / (SC::PIECES * BN);
       const int n = n0 + row < N ? n0 + row : N - 1;
       // a piece past the row's last group (only in the last chunk of a slice
@@ -291,7 +307,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
       // row's last piece instead: in bounds, never used
       const int gp = min(g0 + piece * (SC::SPIECE / 2), G - SC::SPIECE / 2);
       const uint16_t* src = (arr ? biases : scales) + (int64_t)n * G + gp;
-      lds_void* dst = (lds_void*)&Ss[c & 1][((d * kWaves + wave) * 64) * SC::SSTRIDE];
+      lds_void* dst = (lds_void*)&Ss[c & 1][((d * KW + wave) * 64) * SC::SSTRIDE];
       __builtin_amdgcn_global_load_lds((const void*)src, dst, SC::SPIECE, 0, 0);
     }
   };
@@ -300,9 +316,9 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   asm volatile("" : "+v"(mag));
   const h2 k1024 = h2{(_Float16)1024.f, (_Float16)1024.f};
 
-  f32x4 acc[MT][NT];
+  f32x4 acc[MW][NT];
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
+  for (int i = 0; i < MW; ++i)
 #pragma unroll
     for (int u = 0; u < NT; ++u) acc[i][u] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -354,17 +370,17 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
 #pragma unroll
           for (int h = 0; h < LW; ++h) {
             const int gl = (p * kStage + (BITS == 4 ? lg * 32 : h * 64 + lg * 16)) >> LGS;
-            const int row = wave * (NT * 16) + u * 16 + col;
+            const int row = wc * (NT * 16) + u * 16 + col;
             sv[u][h] = lds_u16_nowait(sbuf + SC::offset(0, row, gl));
             bv[u][h] = lds_u16_nowait(sbuf + SC::offset(1, row, gl));
           }
         // activation operand (MFMA A layout: lane (row col, k-block lg)) of
         // m-tile i for step j, from the swizzled slot p
-        u32x4 av[2][MT];
-        auto read_a = [&](u32x4 (&a)[MT], int j) {
+        u32x4 av[2][MW];
+        auto read_a = [&](u32x4 (&a)[MW], int j) {
 #pragma unroll
-          for (int i = 0; i < MT; ++i) {
-            const int m = i * 16 + col, kb = step_off<BITS>(j, lg) >> 3;
+          for (int i = 0; i < MW; ++i) {
+            const int m = (wr * MW + i) * 16 + col, kb = step_off<BITS>(j, lg) >> 3;
             a[i] = lds_b128_nowait(&As[p][m * 16 + (kb ^ (m & 15))]);
           }
         };
@@ -378,7 +394,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
             ready(bv[u][h]);
           }
 #pragma unroll
-        for (int i = 0; i < MT; ++i) ready(av[0][i]);
+        for (int i = 0; i < MW; ++i) ready(av[0][i]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           u32x4 b[NT];
@@ -400,11 +416,11 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
           if (j > 0) {
             lds_wait_all();
 #pragma unroll
-            for (int i = 0; i < MT; ++i) ready(av[j & 1][i]);
+            for (int i = 0; i < MW; ++i) ready(av[j & 1][i]);
           }
           if (j < 3) read_a(av[(j + 1) & 1], j + 1);
 #pragma unroll
-          for (int i = 0; i < MT; ++i)
+          for (int i = 0; i < MW; ++i)
 #pragma unroll
             for (int u = 0; u < NT; ++u) acc[i][u] = mfma_f16(av[j & 1][i], b[u], acc[i][u]);
         }
@@ -433,20 +449,23 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   for (int i0 = 0; i0 < MT; i0 += EP) {
     __syncthreads();
 #pragma unroll
-    for (int i = i0; i < i0 + EP; ++i) {
+    for (int il = 0; il < MW; ++il) {
+      const int i = wr * MW + il;            // m-tile within the workgroup tile
+      if (i < i0 || i >= i0 + EP) continue;  // another pass (uniform per wave)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = (i - i0) * 16 + 4 * lg + e;
         const int m = m0 + i * 16 + 4 * lg + e;
         const float rs = m < M ? rscale[m] : 0.f;
 #pragma unroll
-        for (int u = 0; u < NT; ++u) T[tidx(r, wave * (NT * 16) + u * 16 + col)] = acc[i][u][e] * rs;
+        for (int u = 0; u < NT; ++u) T[tidx(r, wc * (NT * 16) + u * 16 + col)] = acc[il][u][e] * rs;
       }
     }
     __syncthreads();
     constexpr int BLOCKS = EP * 16 * (BN / 4);  // 16-byte blocks of the pass
+    static_assert(BLOCKS % (64 * KW) == 0, "whole rounds of blocks");
 #pragma unroll
-    for (int b0 = 0; b0 < BLOCKS; b0 += 64 * kWaves) {
+    for (int b0 = 0; b0 < BLOCKS; b0 += 64 * KW) {
       const int b = b0 + tid, r = b / (BN / 4), c = (b % (BN / 4)) * 4;
       int m = m0 + i0 * 16 + r;
       const int n = n0 + c;
@@ -529,9 +548,9 @@ template <int BITS, bool SF16, int MT, int GS, int NT, bool GR>
 static hipError_t launch_range(const QmvArgs& a, const GemmPlan& p, const u32x4* xh,
                                const float* rsc, float* part, int tile0, int cnt, int nsplit,
                                const int* gtab, const int* rowmap) {
-  const int total = cnt * (4 / NT) * nsplit;
+  const int total = cnt * (kNT / NT) * nsplit;
   const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
-  hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS, NT, GR>), dim3(grid), dim3(64 * kWaves), 0,
+  hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS, NT, GR>), dim3(grid), dim3(64 * kWaves * wr_for(MT)), 0,
                      a.stream, xh, rsc, (const uint32_t*)a.w, (const uint16_t*)a.scales,
                      (const uint16_t*)a.biases, part, a.out, a.odt, a.M, a.N, a.K, p.kslice,
                      p.tiles_n, tile0, cnt, nsplit, gtab, rowmap);
@@ -543,13 +562,13 @@ static hipError_t launch_mt(const QmvArgs& a, const GemmPlan& p, const u32x4* xh
                             float* part, const int* gtab, const int* rowmap) {
   const int T = p.tiles_n * p.tiles_m;
   if constexpr (GR) {
-    return launch_range<BITS, SF16, MT, GS, 4, true>(a, p, xh, rsc, part, 0, T, 1, gtab, rowmap);
+    return launch_range<BITS, SF16, MT, GS, kNT, true>(a, p, xh, rsc, part, 0, T, 1, gtab, rowmap);
   } else {
     hipError_t e =
-        launch_range<BITS, SF16, MT, GS, 4, false>(a, p, xh, rsc, part, 0, T - p.tail, p.nsplit, nullptr, nullptr);
+        launch_range<BITS, SF16, MT, GS, kNT, false>(a, p, xh, rsc, part, 0, T - p.tail, p.nsplit, nullptr, nullptr);
     if constexpr (MT == kMaxMT) {
       if (e == hipSuccess && p.tail > 0)
-        e = launch_range<BITS, SF16, MT, GS, 2, false>(a, p, xh, rsc, part, T - p.tail, p.tail, 1, nullptr,
+        e = launch_range<BITS, SF16, MT, GS, kNT / 2, false>(a, p, xh, rsc, part, T - p.tail, p.tail, 1, nullptr,
                                                        nullptr);
     }
     return e;
