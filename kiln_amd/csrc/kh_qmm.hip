@@ -115,6 +115,88 @@ __device__ __forceinline__ void prep_row(const uint16_t* __restrict__ x, u32x4* 
   }
 }
 
+// prep_row by one wave, for rows of at most 64 * CPL 16-byte chunks (K <=
+// 512 * CPL): the row is read once into registers, its maximum reduced across
+// the wave's lanes, then converted. Same values as prep_row (the maximum does
+// not depend on the order it is taken in).
+template <int BITS, bool XBF16, int CPL>
+__device__ __forceinline__ void prep_row_wave(const uint16_t* __restrict__ x, u32x4* __restrict__ dst,
+                                              float* __restrict__ rs, int K, bool zero) {
+  const int lane = threadIdx.x & 63;
+  const u32x4* row = reinterpret_cast<const u32x4*>(x);
+  const int nb = K / 8;
+  if (zero) {
+    for (int c = lane; c < nb; c += 64) dst[c] = u32x4{0u, 0u, 0u, 0u};
+    if (lane == 0) *rs = 0.f;
+    return;
+  }
+  u32x4 v[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int i = c * 64 + lane;
+    v[c] = i < nb ? row[i] : u32x4{0u, 0u, 0u, 0u};
+  }
+  float mx = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = XBF16 ? bf16_bits_to_f32(v[c][e] & 0xffffu) : f16_bits_to_f32(v[c][e] & 0xffffu);
+      const float hi = XBF16 ? bf16_bits_to_f32(v[c][e] >> 16) : f16_bits_to_f32(v[c][e] >> 16);
+      mx = fmaxf(mx, fmaxf(fabsf(lo), fabsf(hi)));
+    }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  int ex = 0;
+  if (mx >= 32768.f) {
+    int e2;
+    (void)frexpf(mx, &e2);
+    ex = e2 - 15;
+  }
+  const float inv = ldexpf(1.f, -ex);
+  if (lane == 0) *rs = ldexpf(1.f, ex);
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int i = c * 64 + lane;
+    if (i >= nb) break;
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = XBF16 ? bf16_bits_to_f32(v[c][e] & 0xffffu) : f16_bits_to_f32(v[c][e] & 0xffffu);
+      const float hi = XBF16 ? bf16_bits_to_f32(v[c][e] >> 16) : f16_bits_to_f32(v[c][e] >> 16);
+      o[e] = f32_to_f16_bits(lo * inv) | (f32_to_f16_bits(hi * inv) << 16);
+    }
+    dst[i] = permute_x<BITS>(o);
+  }
+}
+
+// One wave per row, four rows per workgroup.
+template <int BITS, bool XBF16, int CPL>
+__global__ __launch_bounds__(256) void qmm_prep_x_w(const uint16_t* __restrict__ x, u32x4* __restrict__ xh,
+                                                    float* __restrict__ rscale, int M, int K) {
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  prep_row_wave<BITS, XBF16, CPL>(x + (int64_t)m * K, xh + (int64_t)m * (K / 8), rscale + m, K, false);
+}
+
+// group_prep_x with one wave per row.
+template <int BITS, bool XBF16, int CPL>
+__global__ __launch_bounds__(256) void group_prep_x_w(const uint16_t* __restrict__ x, GatherArgs g, int M,
+                                                      const int* __restrict__ pos, u32x4* __restrict__ xh,
+                                                      float* __restrict__ rscale, int* __restrict__ rowmap,
+                                                      int K) {
+  const int64_t rows = g.pairs * M;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * 4) {
+    const int64_t b = r / M;
+    const int i = (int)(r % M);
+    int64_t xo;
+    const int e = gather_expert(g, b, &xo);
+    const int64_t pr = pos[b] + i;
+    prep_row_wave<BITS, XBF16, CPL>(x + xo + (int64_t)i * K, xh + pr * (K / 8), rscale + pr, K, e >= g.E);
+    if ((threadIdx.x & 63) == 0) rowmap[pr] = (int)r;
+  }
+}
+
 // xh[m], rscale[m] = prep_row(x[m]). One workgroup per row.
 template <int BITS, bool XBF16>
 __global__ __launch_bounds__(256) void qmm_prep_x(const uint16_t* __restrict__ x,
@@ -351,36 +433,79 @@ static hipError_t launch_gs(const QmvArgs& a, const u32x4* xh, const float* rsc)
 
 // `ws` holds qmm_workspace_bytes(M, K) bytes (16-byte aligned). Scales and
 // biases are float16 or bfloat16.
+// Chunks per lane of the one-wave row kernels (0: the row is too long for
+// registers and takes the workgroup-per-row kernels).
+static int prep_cpl(int K) {
+  const int nb = K / 8;
+  for (int c : {2, 4, 8, 16, 32})
+    if (nb <= 64 * c) return c;
+  return 0;
+}
+
+template <int BITS, bool X>
+static hipError_t group_prep_b(const QmvArgs& a, const GatherArgs& g, const int* pos, u32x4* xh, float* rsc,
+                               int* rowmap) {
+  const int64_t rows = g.pairs * a.M;
+  const int cpl = prep_cpl(a.K);
+  if (cpl == 0) {
+    const unsigned grid = (unsigned)(rows < (1 << 20) ? rows : (1 << 20));
+    hipLaunchKernelGGL((group_prep_x<BITS, X>), dim3(grid), dim3(256), 0, a.stream, (const uint16_t*)a.x, g,
+                       a.M, pos, xh, rsc, rowmap, a.K);
+    return hipGetLastError();
+  }
+  const int64_t wg = (rows + 3) / 4;
+  const unsigned grid = (unsigned)(wg < (1 << 20) ? wg : (1 << 20));
+#define KH_GW(C)                                                                                      \
+  hipLaunchKernelGGL((group_prep_x_w<BITS, X, C>), dim3(grid), dim3(256), 0, a.stream,                \
+                     (const uint16_t*)a.x, g, a.M, pos, xh, rsc, rowmap, a.K)
+  switch (cpl) {
+    case 2: KH_GW(2); break;
+    case 4: KH_GW(4); break;
+    case 8: KH_GW(8); break;
+    case 16: KH_GW(16); break;
+    default: KH_GW(32); break;
+  }
+#undef KH_GW
+  return hipGetLastError();
+}
+
 hipError_t launch_group_prep_x(const QmvArgs& a, const GatherArgs& g, const int* pos, void* xh_,
                                float* rsc, int* rowmap) {
   u32x4* xh = static_cast<u32x4*>(xh_);
   const bool xbf16 = a.xdt == DT_BF16;
-  const int64_t rows = g.pairs * a.M;
-  const unsigned grid = (unsigned)(rows < (1 << 20) ? rows : (1 << 20));
-#define KH_GPREP(B, X)                                                                              \
-  hipLaunchKernelGGL((group_prep_x<B, X>), dim3(grid), dim3(256), 0, a.stream, (const uint16_t*)a.x, g, \
-                     a.M, pos, xh, rsc, rowmap, a.K)
-  if (a.bits == 4) {
-    if (xbf16) KH_GPREP(4, true); else KH_GPREP(4, false);
-  } else {
-    if (xbf16) KH_GPREP(8, true); else KH_GPREP(8, false);
+  if (a.bits == 4)
+    return xbf16 ? group_prep_b<4, true>(a, g, pos, xh, rsc, rowmap) : group_prep_b<4, false>(a, g, pos, xh, rsc, rowmap);
+  return xbf16 ? group_prep_b<8, true>(a, g, pos, xh, rsc, rowmap) : group_prep_b<8, false>(a, g, pos, xh, rsc, rowmap);
+}
+
+template <int BITS, bool X>
+static hipError_t prep_b(const QmvArgs& a, u32x4* xh, float* rsc) {
+  const int cpl = prep_cpl(a.K);
+  if (cpl == 0) {
+    hipLaunchKernelGGL((qmm_prep_x<BITS, X>), dim3(a.M), dim3(256), 0, a.stream, (const uint16_t*)a.x, xh, rsc,
+                       a.K);
+    return hipGetLastError();
   }
-#undef KH_GPREP
+  const dim3 grid((a.M + 3) / 4);
+#define KH_PW(C)                                                                                    \
+  hipLaunchKernelGGL((qmm_prep_x_w<BITS, X, C>), grid, dim3(256), 0, a.stream, (const uint16_t*)a.x, xh, \
+                     rsc, a.M, a.K)
+  switch (cpl) {
+    case 2: KH_PW(2); break;
+    case 4: KH_PW(4); break;
+    case 8: KH_PW(8); break;
+    case 16: KH_PW(16); break;
+    default: KH_PW(32); break;
+  }
+#undef KH_PW
   return hipGetLastError();
 }
 
 hipError_t launch_prep_x(const QmvArgs& a, void* xh_, float* rsc) {
   u32x4* xh = static_cast<u32x4*>(xh_);
   const bool xbf16 = a.xdt == DT_BF16;
-#define KH_PREP(B, X) \
-  hipLaunchKernelGGL((qmm_prep_x<B, X>), dim3(a.M), dim3(256), 0, a.stream, (const uint16_t*)a.x, xh, rsc, a.K)
-  if (a.bits == 4) {
-    if (xbf16) KH_PREP(4, true); else KH_PREP(4, false);
-  } else {
-    if (xbf16) KH_PREP(8, true); else KH_PREP(8, false);
-  }
-#undef KH_PREP
-  return hipGetLastError();
+  if (a.bits == 4) return xbf16 ? prep_b<4, true>(a, xh, rsc) : prep_b<4, false>(a, xh, rsc);
+  return xbf16 ? prep_b<8, true>(a, xh, rsc) : prep_b<8, false>(a, xh, rsc);
 }
 
 hipError_t launch_qmm(const QmvArgs& a, void* ws) {

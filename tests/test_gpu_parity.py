@@ -105,6 +105,22 @@ def test_qmm_transpose_false(oracle, bits, gs, xdt):
     assert np.array_equal(y, ref)
 
 
+@pytest.mark.parametrize("K", [512, 16384, 16512])
+def test_gemm_activation_prep_row_lengths(oracle, K):
+    """The activation conversion in front of the GEMM: one wave per row up to
+    K = 16384 (the row held in registers), a workgroup per row beyond; rows
+    whose maximum needs the power-of-two scaling (|x| >= 2^15) included."""
+    print(f"case gemm prep K={K}", flush=True)
+    M, N, gs, bits = 40, 48, 64, 4
+    L, x = _case(M, N, K, gs, bits, seed=K)
+    xf = oracle.to_f32(x, "bf16").copy()
+    xf[3] *= 3.0e5
+    xf[17, 5] = -7.0e4
+    x = oracle.from_f32(xf, "bf16")
+    y = _run(L, x, gs, bits, "bf16", "f16", "f32")
+    _check_f32(oracle, L, x, gs, bits, "bf16", "f16", y, rel=F16W_REL)
+
+
 def test_qmm_f32_activations_bit_exact(oracle):
     M, N, K, gs = 3, 40, 256, 32
     L, x = _case(M, N, K, gs, 4, xdt="f32", seed=9)
