@@ -238,6 +238,30 @@ def test_embedding_signed_ids_and_out_of_range():
     assert not y[1, 0].any() and not y[1, 1].any()
 
 
+@pytest.mark.parametrize("H,bits,gs", [(4096, 8, 32), (96, 8, 32), (8320, 4, 128), (64, 4, 32)])
+@pytest.mark.parametrize("sdt,odt", [("f16", "bf16"), ("bf16", "f32"), ("f16", "f16")])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_embedding_rows_match_dequantize(H, bits, gs, sdt, odt, aligned):
+    """The lookup equals the dequantized table's rows bit for bit, for 16-byte
+    and 4-byte aligned tables, with signed and out-of-range ids."""
+    V = 37
+    L = make_linear_numpy(V, H, gs, "emb" if bits == 4 else "q8", seed=H + bits, sdt=sdt)
+    w, s, b = dev(L["w"]), dev(L["scales"], sdt), dev(L["biases"], sdt)
+    full = host(ops.dequantize(w, s, b, gs, bits, out_dtype=odt))
+    if not aligned:  # the same words at a 4-byte (not 16-byte) aligned address
+        buf = torch.zeros(w.numel() + 1, dtype=w.dtype, device="cuda")
+        buf[1:] = w.reshape(-1)
+        w = buf[1:].view(w.shape)
+        assert w.data_ptr() % 16 != 0
+    ids = np.array([5, 0, 36, -1, 37, 12, 5, -40, 20], dtype=np.int32)
+    y = host(ops.quantized_embedding(torch.from_numpy(ids).cuda(), w, s, b, gs, bits, out_dtype=odt))
+    for t, i in enumerate(ids):
+        if -V <= i < V:
+            assert np.array_equal(y[t], full[i % V]), t
+        else:
+            assert not y[t].astype(np.float64).any(), t
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.int32, torch.uint8])
 def test_take_rows(dtype):
     a = (torch.arange(10 * 6, device="cuda") % 251).to(dtype).reshape(10, 6)
