@@ -55,7 +55,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--profile", choices=["decode", "prefill", "traffic"], default=None,
+    ap.add_argument("--profile", choices=["decode", "prefill", "traffic", "moe"], default=None,
                     help="run one workload for a profiler and exit (no JSON line): the M=1 decode "
                          "step, the M=2048 Llama-3-8B layer, or a copy of known size followed by "
                          "gate-shape GEMV launches (counter calibration)")
@@ -199,6 +199,28 @@ def profile_run(kind, torch, ops, layers, shapes, layer_fns, dev, gs, bits):
         step, _ = layer_fns(layers[:2], shapes, 2048, gs, bits)
         for r in range(6):
             step(r % 2)
+    elif kind == "moe":
+        # gather_qmm as SwitchGlu issues it at prefill: OLMoE experts (E=64,
+        # top-8), T = 2048 tokens -> 16384 one-row pairs sorted by expert,
+        # gate/up shape then down shape, 5 calls each
+        from kiln_amd.workloads import make_linear_device
+        E, k, T = 64, 8, 2048
+        g = torch.Generator(device=dev)
+        g.manual_seed(T)
+        ids = torch.stack([torch.randperm(E, device=dev, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+        order = torch.argsort(ids.reshape(-1), stable=True)
+        idx = ids.reshape(-1)[order].contiguous()
+        for Ne, Ke in ((1024, 2048), (2048, 1024)):
+            Ls = [make_linear_device(Ne, Ke, 64, "q4", seed=e) for e in range(E)]
+            we = torch.stack([L["w"] for L in Ls])
+            se = torch.stack([L["scales"] for L in Ls])
+            be = torch.stack([L["biases"] for L in Ls])
+            del Ls
+            xt = torch.randn((T, Ke), device=dev, generator=g).bfloat16()
+            xg = xt[order // k].reshape(T * k, 1, Ke).contiguous()
+            ye = torch.empty((T * k, 1, Ne), dtype=torch.bfloat16, device=dev)
+            for _ in range(5):
+                ops.gather_qmm(xg, we, se, be, idx, True, 64, 4, True, out=ye)
     else:
         # a device-to-device copy of 256 MiB (reads and writes exactly that
         # much: the calibration of FETCH_SIZE / WRITE_SIZE), then 12 launches

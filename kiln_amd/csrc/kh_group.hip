@@ -30,8 +30,13 @@ namespace kh {
 namespace {
 
 constexpr int kPlanThreads = 1024;  // one thread per group in the scan
+constexpr int kChunk = 16;          // ids a thread loads at once
 static_assert(kGroupMaxE + 1 <= kPlanThreads, "one scan slot per group");
 
+// Thread tid takes the contiguous block of pairs [tid * per, (tid+1) * per),
+// reads its ids kChunk at a time (all loads in flight together) and counts
+// runs of equal experts, so sorted ids (SwitchGlu's sort path) cost one LDS
+// atomic per run instead of one per pair on a shared counter.
 __global__ __launch_bounds__(kPlanThreads) void group_plan_kernel(GatherArgs g, int M, int BM,
                                                                   int64_t padded, int* __restrict__ tab,
                                                                   int* __restrict__ pos,
@@ -39,11 +44,35 @@ __global__ __launch_bounds__(kPlanThreads) void group_plan_kernel(GatherArgs g, 
   __shared__ int cnt[kPlanThreads];
   __shared__ int sc[kPlanThreads];
   const int tid = threadIdx.x;
+  const int64_t per = (g.pairs + kPlanThreads - 1) / kPlanThreads;
+  const int64_t b0 = min<int64_t>(g.pairs, tid * per), b1 = min<int64_t>(g.pairs, b0 + per);
   cnt[tid] = 0;
   __syncthreads();
-  for (int64_t b = tid; b < g.pairs; b += kPlanThreads) {
-    int64_t xo;
-    atomicAdd(&cnt[gather_expert(g, b, &xo)], 1);
+  // experts of pairs base .. base+kChunk-1 (-1 past the block), loaded together
+  auto chunk = [&](int64_t base, int (&ev)[kChunk]) {
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      int64_t xo;
+      ev[j] = base + j < b1 ? gather_expert(g, base + j, &xo) : -1;
+    }
+  };
+  {
+    int run_e = -1, run_n = 0;
+    for (int64_t base = b0; base < b1; base += kChunk) {
+      int ev[kChunk];
+      chunk(base, ev);
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j) {
+        if (ev[j] < 0) break;
+        if (ev[j] != run_e) {
+          if (run_n) atomicAdd(&cnt[run_e], run_n);
+          run_e = ev[j];
+          run_n = 0;
+        }
+        ++run_n;
+      }
+    }
+    if (run_n) atomicAdd(&cnt[run_e], run_n);
   }
   __syncthreads();
   // m-tiles of group tid, then their inclusive prefix sum (Hillis-Steele)
@@ -64,10 +93,23 @@ __global__ __launch_bounds__(kPlanThreads) void group_plan_kernel(GatherArgs g, 
   sc[tid] = t0 * BM;   // now the first padded row of each group
   __syncthreads();
   for (int64_t r = tid; r < padded; r += kPlanThreads) rowmap[r] = -1;
-  for (int64_t b = tid; b < g.pairs; b += kPlanThreads) {
-    int64_t xo;
-    const int e = gather_expert(g, b, &xo);
-    pos[b] = sc[e] + atomicAdd(&cnt[e], 1) * M;
+  // slots: one atomic per run (within a chunk) reserves its consecutive slots
+  for (int64_t base = b0; base < b1; base += kChunk) {
+    int ev[kChunk];
+    chunk(base, ev);
+    int cur = ev[0], j0 = 0;  // the run being scanned: expert, first index
+#pragma unroll
+    for (int j = 1; j <= kChunk; ++j) {
+      const int ej = j < kChunk ? ev[j] : -2;
+      if (ej != cur) {
+        if (cur >= 0) {
+          const int first = atomicAdd(&cnt[cur], j - j0);
+          for (int q = j0; q < j; ++q) pos[base + q] = sc[cur] + (first + q - j0) * M;
+        }
+        cur = ej;
+        j0 = j;
+      }
+    }
   }
 }
 

@@ -58,11 +58,16 @@ struct GatherArgs {
 // element offset into x.
 __device__ __forceinline__ int gather_expert(const GatherArgs& g, int64_t b, int64_t* xo) {
   int64_t xoff = 0, io = 0, rem = b;
-  for (int d = g.nd - 1; d >= 0; --d) {
-    const int64_t c = rem % g.shape[d];
-    rem /= g.shape[d];
-    xoff += c * g.xs[d];
-    io += c * g.is[d];
+  if (g.nd == 1) {  // one batch dimension (b < shape[0]): no division
+    xoff = b * g.xs[0];
+    io = b * g.is[0];
+  } else {
+    for (int d = g.nd - 1; d >= 0; --d) {
+      const int64_t c = rem % g.shape[d];
+      rem /= g.shape[d];
+      xoff += c * g.xs[d];
+      io += c * g.is[d];
+    }
   }
   int64_t e = g.idx_signed ? (int64_t) static_cast<const int32_t*>(g.idx)[io]
                            : (int64_t) static_cast<const uint32_t*>(g.idx)[io];

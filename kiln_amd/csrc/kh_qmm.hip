@@ -115,25 +115,27 @@ __device__ __forceinline__ void prep_row(const uint16_t* __restrict__ x, u32x4* 
   }
 }
 
-// prep_row by one wave, for rows of at most 64 * CPL 16-byte chunks (K <=
-// 512 * CPL): the row is read once into registers, its maximum reduced across
-// the wave's lanes, then converted. Same values as prep_row (the maximum does
-// not depend on the order it is taken in).
-template <int BITS, bool XBF16, int CPL>
-__device__ __forceinline__ void prep_row_wave(const uint16_t* __restrict__ x, u32x4* __restrict__ dst,
-                                              float* __restrict__ rs, int K, bool zero) {
-  const int lane = threadIdx.x & 63;
+// prep_row by WPR waves (64 * WPR threads per row, WPR = 1 or 4), for rows
+// of at most 64 * WPR * CPL 16-byte chunks: the row is read once into
+// registers and its maximum reduced across lanes (and, for WPR = 4, across
+// the workgroup's waves through LDS), then converted. Same values as
+// prep_row: the maximum does not depend on the order it is taken in.
+template <int BITS, bool XBF16, int CPL, int WPR>
+__device__ __forceinline__ void prep_row_regs(const uint16_t* __restrict__ x, u32x4* __restrict__ dst,
+                                              float* __restrict__ rs, int K, bool zero, float* red) {
+  constexpr int TPR = 64 * WPR;  // threads per row
+  const int tr = threadIdx.x % TPR;
   const u32x4* row = reinterpret_cast<const u32x4*>(x);
   const int nb = K / 8;
-  if (zero) {
-    for (int c = lane; c < nb; c += 64) dst[c] = u32x4{0u, 0u, 0u, 0u};
-    if (lane == 0) *rs = 0.f;
+  if (zero) {  // uniform across the row's threads
+    for (int c = tr; c < nb; c += TPR) dst[c] = u32x4{0u, 0u, 0u, 0u};
+    if (tr == 0) *rs = 0.f;
     return;
   }
   u32x4 v[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    const int i = c * 64 + lane;
+    const int i = c * TPR + tr;
     v[c] = i < nb ? row[i] : u32x4{0u, 0u, 0u, 0u};
   }
   float mx = 0.f;
@@ -147,6 +149,13 @@ __device__ __forceinline__ void prep_row_wave(const uint16_t* __restrict__ x, u3
     }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  if constexpr (WPR > 1) {
+    if ((tr & 63) == 0) red[tr >> 6] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < WPR; ++w) mx = fmaxf(mx, red[w]);
+    __syncthreads();  // red is reused by the next row
+  }
   int ex = 0;
   if (mx >= 32768.f) {
     int e2;
@@ -154,10 +163,10 @@ __device__ __forceinline__ void prep_row_wave(const uint16_t* __restrict__ x, u3
     ex = e2 - 15;
   }
   const float inv = ldexpf(1.f, -ex);
-  if (lane == 0) *rs = ldexpf(1.f, ex);
+  if (tr == 0) *rs = ldexpf(1.f, ex);
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    const int i = c * 64 + lane;
+    const int i = c * TPR + tr;
     if (i >= nb) break;
     u32x4 o;
 #pragma unroll
@@ -170,30 +179,37 @@ __device__ __forceinline__ void prep_row_wave(const uint16_t* __restrict__ x, u3
   }
 }
 
-// One wave per row, four rows per workgroup.
-template <int BITS, bool XBF16, int CPL>
+// 4 / WPR rows per workgroup of 256 threads.
+template <int BITS, bool XBF16, int CPL, int WPR>
 __global__ __launch_bounds__(256) void qmm_prep_x_w(const uint16_t* __restrict__ x, u32x4* __restrict__ xh,
                                                     float* __restrict__ rscale, int M, int K) {
-  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (m >= M) return;
-  prep_row_wave<BITS, XBF16, CPL>(x + (int64_t)m * K, xh + (int64_t)m * (K / 8), rscale + m, K, false);
+  __shared__ float red[4];
+  const int m = blockIdx.x * (4 / WPR) + (int)threadIdx.x / (64 * WPR);
+  if (m >= M) return;  // WPR = 4: uniform per workgroup
+  prep_row_regs<BITS, XBF16, CPL, WPR>(x + (int64_t)m * K, xh + (int64_t)m * (K / 8), rscale + m, K, false,
+                                       red);
 }
 
-// group_prep_x with one wave per row.
-template <int BITS, bool XBF16, int CPL>
+// group_prep_x with the row kernels' layout.
+template <int BITS, bool XBF16, int CPL, int WPR>
 __global__ __launch_bounds__(256) void group_prep_x_w(const uint16_t* __restrict__ x, GatherArgs g, int M,
                                                       const int* __restrict__ pos, u32x4* __restrict__ xh,
                                                       float* __restrict__ rscale, int* __restrict__ rowmap,
                                                       int K) {
+  __shared__ float red[4];
+  constexpr int RPW = 4 / WPR;  // rows per workgroup and step
   const int64_t rows = g.pairs * M;
-  for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * 4) {
+  // every thread of a row (for WPR = 4: of the workgroup) runs the same trips
+  for (int64_t r = (int64_t)blockIdx.x * RPW + (int)threadIdx.x / (64 * WPR); r < rows;
+       r += (int64_t)gridDim.x * RPW) {
     const int64_t b = r / M;
     const int i = (int)(r % M);
     int64_t xo;
     const int e = gather_expert(g, b, &xo);
     const int64_t pr = pos[b] + i;
-    prep_row_wave<BITS, XBF16, CPL>(x + xo + (int64_t)i * K, xh + pr * (K / 8), rscale + pr, K, e >= g.E);
-    if ((threadIdx.x & 63) == 0) rowmap[pr] = (int)r;
+    prep_row_regs<BITS, XBF16, CPL, WPR>(x + xo + (int64_t)i * K, xh + pr * (K / 8), rscale + pr, K,
+                                         e >= g.E, red);
+    if ((int)threadIdx.x % (64 * WPR) == 0) rowmap[pr] = (int)r;
   }
 }
 
@@ -433,37 +449,40 @@ static hipError_t launch_gs(const QmvArgs& a, const u32x4* xh, const float* rsc)
 
 // `ws` holds qmm_workspace_bytes(M, K) bytes (16-byte aligned). Scales and
 // biases are float16 or bfloat16.
-// Chunks per lane of the one-wave row kernels (0: the row is too long for
-// registers and takes the workgroup-per-row kernels).
-static int prep_cpl(int K) {
+// Layout of the register row kernels: (chunks per lane, waves per row), or
+// cpl = 0 when the row is too long for registers (workgroup-per-row kernels).
+struct PrepShape {
+  int cpl, wpr;
+};
+static PrepShape prep_shape(int K) {
   const int nb = K / 8;
-  for (int c : {2, 4, 8, 16, 32})
-    if (nb <= 64 * c) return c;
-  return 0;
+  for (int c : {2, 4, 8})
+    if (nb <= 64 * c) return {c, 1};
+  for (int c : {4, 8})
+    if (nb <= 256 * c) return {c, 4};
+  return {0, 0};
 }
 
 template <int BITS, bool X>
 static hipError_t group_prep_b(const QmvArgs& a, const GatherArgs& g, const int* pos, u32x4* xh, float* rsc,
                                int* rowmap) {
   const int64_t rows = g.pairs * a.M;
-  const int cpl = prep_cpl(a.K);
-  if (cpl == 0) {
+  const PrepShape ps = prep_shape(a.K);
+  if (ps.cpl == 0) {
     const unsigned grid = (unsigned)(rows < (1 << 20) ? rows : (1 << 20));
     hipLaunchKernelGGL((group_prep_x<BITS, X>), dim3(grid), dim3(256), 0, a.stream, (const uint16_t*)a.x, g,
                        a.M, pos, xh, rsc, rowmap, a.K);
     return hipGetLastError();
   }
-  const int64_t wg = (rows + 3) / 4;
+  const int64_t wg = ps.wpr == 1 ? (rows + 3) / 4 : rows;
   const unsigned grid = (unsigned)(wg < (1 << 20) ? wg : (1 << 20));
-#define KH_GW(C)                                                                                      \
-  hipLaunchKernelGGL((group_prep_x_w<BITS, X, C>), dim3(grid), dim3(256), 0, a.stream,                \
+#define KH_GW(C, W)                                                                                   \
+  hipLaunchKernelGGL((group_prep_x_w<BITS, X, C, W>), dim3(grid), dim3(256), 0, a.stream,             \
                      (const uint16_t*)a.x, g, a.M, pos, xh, rsc, rowmap, a.K)
-  switch (cpl) {
-    case 2: KH_GW(2); break;
-    case 4: KH_GW(4); break;
-    case 8: KH_GW(8); break;
-    case 16: KH_GW(16); break;
-    default: KH_GW(32); break;
+  if (ps.wpr == 1) {
+    if (ps.cpl == 2) KH_GW(2, 1); else if (ps.cpl == 4) KH_GW(4, 1); else KH_GW(8, 1);
+  } else {
+    if (ps.cpl == 4) KH_GW(4, 4); else KH_GW(8, 4);
   }
 #undef KH_GW
   return hipGetLastError();
@@ -480,22 +499,20 @@ hipError_t launch_group_prep_x(const QmvArgs& a, const GatherArgs& g, const int*
 
 template <int BITS, bool X>
 static hipError_t prep_b(const QmvArgs& a, u32x4* xh, float* rsc) {
-  const int cpl = prep_cpl(a.K);
-  if (cpl == 0) {
+  const PrepShape ps = prep_shape(a.K);
+  if (ps.cpl == 0) {
     hipLaunchKernelGGL((qmm_prep_x<BITS, X>), dim3(a.M), dim3(256), 0, a.stream, (const uint16_t*)a.x, xh, rsc,
                        a.K);
     return hipGetLastError();
   }
-  const dim3 grid((a.M + 3) / 4);
-#define KH_PW(C)                                                                                    \
-  hipLaunchKernelGGL((qmm_prep_x_w<BITS, X, C>), grid, dim3(256), 0, a.stream, (const uint16_t*)a.x, xh, \
+  const dim3 grid(ps.wpr == 1 ? (a.M + 3) / 4 : a.M);
+#define KH_PW(C, W)                                                                                 \
+  hipLaunchKernelGGL((qmm_prep_x_w<BITS, X, C, W>), grid, dim3(256), 0, a.stream, (const uint16_t*)a.x, xh, \
                      rsc, a.M, a.K)
-  switch (cpl) {
-    case 2: KH_PW(2); break;
-    case 4: KH_PW(4); break;
-    case 8: KH_PW(8); break;
-    case 16: KH_PW(16); break;
-    default: KH_PW(32); break;
+  if (ps.wpr == 1) {
+    if (ps.cpl == 2) KH_PW(2, 1); else if (ps.cpl == 4) KH_PW(4, 1); else KH_PW(8, 1);
+  } else {
+    if (ps.cpl == 4) KH_PW(4, 4); else KH_PW(8, 4);
   }
 #undef KH_PW
   return hipGetLastError();

@@ -105,11 +105,12 @@ def test_qmm_transpose_false(oracle, bits, gs, xdt):
     assert np.array_equal(y, ref)
 
 
-@pytest.mark.parametrize("K", [512, 16384, 16512])
+@pytest.mark.parametrize("K", [512, 6144, 16384, 16512])
 def test_gemm_activation_prep_row_lengths(oracle, K):
-    """The activation conversion in front of the GEMM: one wave per row up to
-    K = 16384 (the row held in registers), a workgroup per row beyond; rows
-    whose maximum needs the power-of-two scaling (|x| >= 2^15) included."""
+    """The activation conversion in front of the GEMM: rows held in registers
+    by one wave (K <= 4096) or four waves (K <= 16384), a workgroup per row
+    beyond; rows whose maximum needs the power-of-two scaling (|x| >= 2^15)
+    included."""
     print(f"case gemm prep K={K}", flush=True)
     M, N, gs, bits = 40, 48, 64, 4
     L, x = _case(M, N, K, gs, bits, seed=K)
