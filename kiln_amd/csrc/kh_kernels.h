@@ -54,26 +54,35 @@ struct GatherArgs {
   int shape[8];
   int64_t xs[8], is[8];
 };
-// Expert of pair b (g.E when the id is outside [-E, E)); *xo = the pair's
-// element offset into x.
-__device__ __forceinline__ int gather_expert(const GatherArgs& g, int64_t b, int64_t* xo) {
-  int64_t xoff = 0, io = 0, rem = b;
+// Element offset of pair b's id in idx; *xo = the pair's element offset in x.
+__device__ __forceinline__ int64_t gather_io(const GatherArgs& g, int64_t b, int64_t* xo) {
   if (g.nd == 1) {  // one batch dimension (b < shape[0]): no division
-    xoff = b * g.xs[0];
-    io = b * g.is[0];
-  } else {
-    for (int d = g.nd - 1; d >= 0; --d) {
-      const int64_t c = rem % g.shape[d];
-      rem /= g.shape[d];
-      xoff += c * g.xs[d];
-      io += c * g.is[d];
-    }
+    *xo = b * g.xs[0];
+    return b * g.is[0];
   }
-  int64_t e = g.idx_signed ? (int64_t) static_cast<const int32_t*>(g.idx)[io]
-                           : (int64_t) static_cast<const uint32_t*>(g.idx)[io];
-  if (e < 0) e += g.E;
+  int64_t xoff = 0, io = 0, rem = b;
+  for (int d = g.nd - 1; d >= 0; --d) {
+    const int64_t c = rem % g.shape[d];
+    rem /= g.shape[d];
+    xoff += c * g.xs[d];
+    io += c * g.is[d];
+  }
   *xo = xoff;
+  return io;
+}
+__device__ __forceinline__ int gather_raw(const GatherArgs& g, int64_t io) {
+  return g.idx_signed ? static_cast<const int32_t*>(g.idx)[io]
+                      : (int)static_cast<const uint32_t*>(g.idx)[io];
+}
+// Expert of a raw id (g.E when the id is outside [-E, E)).
+__device__ __forceinline__ int gather_to_expert(const GatherArgs& g, int raw) {
+  int64_t e = g.idx_signed ? (int64_t)raw : (int64_t)(uint32_t)raw;
+  if (e < 0) e += g.E;
   return e >= 0 && e < g.E ? (int)e : g.E;
+}
+// Expert of pair b; *xo = the pair's element offset in x.
+__device__ __forceinline__ int gather_expert(const GatherArgs& g, int64_t b, int64_t* xo) {
+  return gather_to_expert(g, gather_raw(g, gather_io(g, b, xo)));
 }
 hipError_t launch_gemv_gather(const QmvArgs& a, const GatherArgs& g);
 // Any dtype/alignment/M: one thread per output, float32 fma chain.
