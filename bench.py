@@ -176,7 +176,7 @@ def main():
                      # HBM bytes per gate launch, FETCH_SIZE + WRITE_SIZE scaled by
                      # what they read for a 256 MiB copy (x1.99976 and x1.0)
                      "traffic": GATE_TRAFFIC_BYTES,
-                     "kernel": "gemv_kernel<4,bf16,f16,M=1,R=8,I=1> at gate 14336x4096",
+                     "kernel": "gemv_kernel<4,bf16,f16,M=1,R=4,I=1> at gate 14336x4096",
                      "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 3)},
         "per_shape_us": {k: round(v, 2) for k, v in per_shape_us.items()},
         "per_shape_gbs": {n: round(call_bytes(N, K, 1, bits, gs) / (per_shape_us[n] * 1e-6) / 1e9, 1)
