@@ -35,7 +35,7 @@ sys.path.insert(0, ROOT)
 
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of `bench.py --profile traffic`:
 # 16,212.5 KiB read x 1.99976 + 56 KiB written, per launch of the gate GEMV
-GATE_TRAFFIC_BYTES = 33_257_515
+GATE_TRAFFIC_BYTES = 33_289_353
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 600_000_000  # rotate over more distinct weight bytes than the 256 MB MALL
