@@ -137,6 +137,12 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 #ifndef KH_GEMM_TAIL
 #define KH_GEMM_TAIL 1  // run a partial last round of 128-row tiles as half-width workgroups
 #endif
+#ifndef KH_GEMM_SPREAD
+#define KH_GEMM_SPREAD 1  // issue each stage's loads spread over the MFMA steps (128-row tiles)
+#endif
+#ifndef KH_GEMM_SPREAD4
+#define KH_GEMM_SPREAD4 1  // ... also for 64-row tiles
+#endif
 #ifndef KH_GEMM_P
 #define KH_GEMM_P 0   // tuning: force the ring depth of 128-row tiles (0 = by tile size)
 #endif
@@ -312,6 +318,29 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
     }
   };
 
+  // Part j (of 4) of a stage's activation and code loads, for issuing a
+  // stage's loads spread over the MFMA steps of the stage before.
+  auto load_acts_part = [&](int buf, int st, int j) {
+    const int kc8 = (k0 + st * kStage) >> 3;
+#pragma unroll
+    for (int d = j * (DOPS / 4); d < (j + 1) * (DOPS / 4); ++d) {
+      const int s = (d * KW + wave) * 64 + lane;
+      const int m = s >> 4, kb = (s & 15) ^ (m & 15);
+      const int mm = m0 + m < M ? m0 + m : M - 1;
+      __builtin_amdgcn_global_load_lds((const void*)(xh + (int64_t)mm * KB8 + kc8 + kb),
+                                       (lds_void*)&As[buf][(d * KW + wave) * 64], 16, 0, 0);
+    }
+  };
+  auto load_codes_part = [&](u32x4 (&q)[NT][LW], int st, int j) {
+    const int kc = k0 + st * kStage;
+    const uint32_t* row = w + (int64_t)nrow[j] * wpr;
+#pragma unroll
+    for (int h = 0; h < LW; ++h) {
+      const int code = kc + (BITS == 4 ? lg * 32 : h * 64 + lg * 16);
+      q[j][h] = *reinterpret_cast<const u32x4*>(row + code * BITS / 32);
+    }
+  };
+
   uint32_t mag = 0x64006400u;  // float16 1024.0 in both halves
   asm volatile("" : "+v"(mag));
   const h2 k1024 = h2{(_Float16)1024.f, (_Float16)1024.f};
@@ -335,6 +364,18 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
   constexpr int OPS = LW * NT;
   constexpr int BASE = OPS + (P - 2) * (DOPS + OPS);
   static_assert(BASE + SC::OPS < 64, "vmcnt holds 6 bits");
+  // Spread issue (128-row, 256-column tiles, one wave per SIMD): the loads
+  // of stage st + P - 1 are issued in four parts, part j
+  // (activation loads j*DOPS/4 .., code tile j) before MFMA step j of stage
+  // st, after the scale chunk when p == 0. The last activation load of a
+  // stage is then followed by its last code load and the P - 2 younger
+  // stages' loads, plus one scale chunk when one of those was issued at
+  // p == 0 (1 <= p <= P - 2).
+  constexpr bool SPREAD = KH_GEMM_SPREAD && (MT == 8 || (KH_GEMM_SPREAD4 && MT == 4)) && NT == 4 && WR == 1 &&
+                          DOPS % 4 == 0;
+  constexpr bool FINE = SPREAD && KH_GEMM_SPREAD == 2 && DOPS % 8 == 0;  // each part split in two around half the MFMAs
+  constexpr int WS0 = OPS / NT + (P - 2) * (DOPS + OPS);
+  static_assert(WS0 + SC::OPS < 64, "vmcnt holds 6 bits");
   load_scales(0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -349,17 +390,53 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const int st = c * P + p;
-      if (p == 0)
-        waitcnt_vm<BASE>();
-      else
-        waitcnt_vm<BASE + SC::OPS>();
+      if constexpr (SPREAD) {
+        if (p >= 1 && p <= P - 2)
+          waitcnt_vm<WS0 + SC::OPS>();
+        else
+          waitcnt_vm<WS0>();
+      } else {
+        if (p == 0)
+          waitcnt_vm<BASE>();
+        else
+          waitcnt_vm<BASE + SC::OPS>();
+      }
       __builtin_amdgcn_s_barrier();
       const int pn = (p + P - 1) % P;  // slot and buffer of stage st + P - 1 (constant once unrolled)
-      load_acts(pn, min(st + P - 1, nst - 1));
-      if (p == 0) load_scales(min(c + 1, nchunks - 1));
-      load_codes(q[pn], min(st + P - 1, nst - 1));
+      const int stn = min(st + P - 1, nst - 1);
+      auto issue = [&](int j) {  // part j of the spread issue
+        if (j == 0 && p == 0) load_scales(min(c + 1, nchunks - 1));
+        load_acts_part(pn, stn, j);
+        load_codes_part(q[pn], stn, j);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      // FINE: the first half of part j's activation loads before step j's
+      // MFMAs, the rest of the part after half of them (same program order)
+      auto issue_half = [&](int j, int h) {
+        if (h == 0 && j == 0 && p == 0) load_scales(min(c + 1, nchunks - 1));
+        const int kc8 = (k0 + stn * kStage) >> 3;
+#pragma unroll
+        for (int d = j * (DOPS / 4) + h * (DOPS / 8); d < j * (DOPS / 4) + (h + 1) * (DOPS / 8); ++d) {
+          const int s = (d * KW + wave) * 64 + lane;
+          const int m = s >> 4, kb = (s & 15) ^ (m & 15);
+          const int mm = m0 + m < M ? m0 + m : M - 1;
+          __builtin_amdgcn_global_load_lds((const void*)(xh + (int64_t)mm * KB8 + kc8 + kb),
+                                           (lds_void*)&As[pn][(d * KW + wave) * 64], 16, 0, 0);
+        }
+        if (h == 1) load_codes_part(q[pn], stn, j);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      if constexpr (!SPREAD) {
+        load_acts(pn, stn);
+        if (p == 0) load_scales(min(c + 1, nchunks - 1));
+        load_codes(q[pn], stn);
+      }
       // The waits above rely on program order of the vector memory ops.
       __builtin_amdgcn_sched_barrier(0);
+      if (SPREAD && st >= nst) {  // uniform: nothing to compute, the loads still go out
+#pragma unroll
+        for (int j = 0; j < 4; ++j) issue(j);
+      }
       if (st < nst) {  // uniform
         const unsigned char* sbuf = &Ss[c & 1][0];
         // this lane's scale and bias for each of its code runs in the stage
@@ -397,6 +474,8 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
         for (int i = 0; i < MW; ++i) ready(av[0][i]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
+          if constexpr (FINE) issue_half(j, 0);
+          else if constexpr (SPREAD) issue(j);
           u32x4 b[NT];
 #pragma unroll
           for (int u = 0; u < NT; ++u) {
@@ -420,9 +499,11 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
           }
           if (j < 3) read_a(av[(j + 1) & 1], j + 1);
 #pragma unroll
-          for (int i = 0; i < MW; ++i)
+          for (int i = 0; i < MW; ++i) {
+            if (FINE && i == MW / 2) issue_half(j, 1);
 #pragma unroll
             for (int u = 0; u < NT; ++u) acc[i][u] = mfma_f16(av[j & 1][i], b[u], acc[i][u]);
+          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);
