@@ -549,6 +549,32 @@ def test_gather_qmm_grouped_ids_out_of_range(oracle):
         _check_f32(oracle, L, xs[p:p + 1], 64, 4, "bf16", "f16", y[p:p + 1], rel=F16W_REL)
 
 
+@pytest.mark.parametrize("E", [300, 1023, 1030])
+def test_gather_qmm_many_experts(oracle, E):
+    """Hundreds of experts through the grouped path (one scan thread per
+    expert group, up to 1023 experts plus the out-of-range group), and past
+    that limit the pair-by-pair kernels: every row equals
+    kh_quantized_matmul on its expert within that kernel's bound."""
+    N, K = 32, 256
+    P = 2 * (E + 1) + 40  # enough rows per group for the grouped path where E allows it
+    w, s, b = _experts(E, N, K, 64, 4, seed=120)
+    rng = np.random.default_rng(121)
+    ids = np.sort(rng.integers(0, E, P)).astype(np.int32)
+    ids[::97] = E + 5  # out of range
+    xs = make_x_numpy(P, K, seed=122, xdt="bf16")
+    y = host(ops.gather_qmm(dev(xs.reshape(P, 1, K), "bf16"), dev(w), dev(s, "f16"), dev(b, "f16"),
+                            torch.from_numpy(ids).cuda(), True, 64, 4, True, out_dtype="f32")).reshape(P, N)
+    assert not y[::97].any()
+    grouped = E <= 1023 and P >= 2 * min(E + 1, P)
+    for p in [1, 2, 50, 333, P - 1]:
+        if p % 97 == 0:
+            continue
+        e = int(ids[p])
+        L = dict(w=w[e], scales=s[e], biases=b[e])
+        _check_f32(oracle, L, xs[p:p + 1], 64, 4, "bf16", "f16", y[p:p + 1],
+                   rel=F16W_REL if grouped else EXACT_REL)
+
+
 def test_gather_qmm_empty_and_errors():
     w, s, b = _experts(2, 32, 256, 64, 4, seed=90)
     W = (dev(w), dev(s, "f16"), dev(b, "f16"))
