@@ -143,6 +143,9 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 #ifndef KH_GEMM_SPREAD4
 #define KH_GEMM_SPREAD4 1  // ... also for 64-row tiles
 #endif
+#ifndef KH_GEMM_IL
+#define KH_GEMM_IL 2  // VALU ops scheduled after each MFMA when dequantising a step ahead (0: off)
+#endif
 #ifndef KH_GEMM_P
 #define KH_GEMM_P 0   // tuning: force the ring depth of 128-row tiles (0 = by tile size)
 #endif
@@ -373,8 +376,10 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
   // p == 0 (1 <= p <= P - 2).
   constexpr bool SPREAD = KH_GEMM_SPREAD && (MT == 8 || (KH_GEMM_SPREAD4 && MT == 4)) && NT == 4 && WR == 1 &&
                           DOPS % 4 == 0;
-  constexpr bool FINE = SPREAD && KH_GEMM_SPREAD == 2 && DOPS % 8 == 0;  // each part split in two around half the MFMAs
   constexpr int WS0 = OPS / NT + (P - 2) * (DOPS + OPS);
+  // dequantisation a step ahead (measured 2-6% on the 4-bit gs64 prefill
+  // shapes; group size 32 would spill with it)
+  constexpr int IL = GS >= 64 ? KH_GEMM_IL : 0;
   static_assert(WS0 + SC::OPS < 64, "vmcnt holds 6 bits");
   load_scales(0);
   __builtin_amdgcn_sched_barrier(0);
@@ -408,22 +413,6 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
         if (j == 0 && p == 0) load_scales(min(c + 1, nchunks - 1));
         load_acts_part(pn, stn, j);
         load_codes_part(q[pn], stn, j);
-        __builtin_amdgcn_sched_barrier(0);
-      };
-      // FINE: the first half of part j's activation loads before step j's
-      // MFMAs, the rest of the part after half of them (same program order)
-      auto issue_half = [&](int j, int h) {
-        if (h == 0 && j == 0 && p == 0) load_scales(min(c + 1, nchunks - 1));
-        const int kc8 = (k0 + stn * kStage) >> 3;
-#pragma unroll
-        for (int d = j * (DOPS / 4) + h * (DOPS / 8); d < j * (DOPS / 4) + (h + 1) * (DOPS / 8); ++d) {
-          const int s = (d * KW + wave) * 64 + lane;
-          const int m = s >> 4, kb = (s & 15) ^ (m & 15);
-          const int mm = m0 + m < M ? m0 + m : M - 1;
-          __builtin_amdgcn_global_load_lds((const void*)(xh + (int64_t)mm * KB8 + kc8 + kb),
-                                           (lds_void*)&As[pn][(d * KW + wave) * 64], 16, 0, 0);
-        }
-        if (h == 1) load_codes_part(q[pn], stn, j);
         __builtin_amdgcn_sched_barrier(0);
       };
       if constexpr (!SPREAD) {
@@ -472,11 +461,8 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
           }
 #pragma unroll
         for (int i = 0; i < MW; ++i) ready(av[0][i]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if constexpr (FINE) issue_half(j, 0);
-          else if constexpr (SPREAD) issue(j);
-          u32x4 b[NT];
+        // dequantised code operand (MFMA B layout) of each column tile for step j
+        auto dequant = [&](u32x4 (&b)[NT], int j) {
 #pragma unroll
           for (int u = 0; u < NT; ++u) {
             const int h = BITS == 4 ? 0 : (j >> 1);
@@ -491,6 +477,15 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
               b[u][e] = __builtin_bit_cast(
                   uint32_t, __builtin_elementwise_fma(s2, __builtin_bit_cast(h2, r[e]) - k1024, b2));
           }
+        };
+        // IL: the operands of step j+1 are dequantised while the MFMAs of
+        // step j run, interleaved by the scheduler (KH_GEMM_IL VALU ops per MFMA)
+        u32x4 bq[2][NT];
+        if constexpr (IL > 0) dequant(bq[0], 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (SPREAD) issue(j);
+          if constexpr (IL == 0) dequant(bq[j & 1], j);
           // operands of step j were read during step j-1 (or above)
           if (j > 0) {
             lds_wait_all();
@@ -498,11 +493,18 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
             for (int i = 0; i < MW; ++i) ready(av[j & 1][i]);
           }
           if (j < 3) read_a(av[(j + 1) & 1], j + 1);
+          if constexpr (IL > 0)
+            if (j < 3) dequant(bq[(j + 1) & 1], j + 1);
 #pragma unroll
-          for (int i = 0; i < MW; ++i) {
-            if (FINE && i == MW / 2) issue_half(j, 1);
+          for (int i = 0; i < MW; ++i)
 #pragma unroll
-            for (int u = 0; u < NT; ++u) acc[i][u] = mfma_f16(av[j & 1][i], b[u], acc[i][u]);
+            for (int u = 0; u < NT; ++u) acc[i][u] = mfma_f16(av[j & 1][i], bq[j & 1][u], acc[i][u]);
+          if constexpr (IL > 0) {
+#pragma unroll
+            for (int i = 0; i < MW * NT; ++i) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+              __builtin_amdgcn_sched_group_barrier(0x002, IL, 0);  // then VALU
+            }
           }
         }
       }
