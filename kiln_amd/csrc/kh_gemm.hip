@@ -140,6 +140,9 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 #ifndef KH_GEMM_SPREAD
 #define KH_GEMM_SPREAD 1  // issue each stage's loads spread over the MFMA steps (128-row tiles)
 #endif
+#ifndef KH_GEMM_SPREAD2
+#define KH_GEMM_SPREAD2 1  // ... also for the half-width tail workgroups
+#endif
 #ifndef KH_GEMM_SPREAD4
 #define KH_GEMM_SPREAD4 1  // ... also for 64-row tiles
 #endif
@@ -335,6 +338,7 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
     }
   };
   auto load_codes_part = [&](u32x4 (&q)[NT][LW], int st, int j) {
+    if (j >= NT) return;
     const int kc = k0 + st * kStage;
     const uint32_t* row = w + (int64_t)nrow[j] * wpr;
 #pragma unroll
@@ -374,9 +378,10 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
   // stage is then followed by its last code load and the P - 2 younger
   // stages' loads, plus one scale chunk when one of those was issued at
   // p == 0 (1 <= p <= P - 2).
-  constexpr bool SPREAD = KH_GEMM_SPREAD && (MT == 8 || (KH_GEMM_SPREAD4 && MT == 4)) && NT == 4 && WR == 1 &&
-                          DOPS % 4 == 0;
-  constexpr int WS0 = OPS / NT + (P - 2) * (DOPS + OPS);
+  constexpr bool SPREAD = KH_GEMM_SPREAD && (MT == 8 || (KH_GEMM_SPREAD4 && MT == 4)) &&
+                          (NT == 4 || (KH_GEMM_SPREAD2 && NT == 2)) && WR == 1 && DOPS % 4 == 0;
+  // (code tile j goes out in part j: with NT = 2 parts 2 and 3 carry none)
+  constexpr int WS0 = (NT == 4 ? LW : 0) + (P - 2) * (DOPS + OPS);
   // dequantisation a step ahead (measured 2-6% on the 4-bit gs64 prefill
   // shapes; group size 32 would spill with it)
   constexpr int IL = GS >= 64 ? KH_GEMM_IL : 0;
