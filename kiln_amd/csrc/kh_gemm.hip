@@ -384,7 +384,7 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
   constexpr int WS0 = (NT == 4 ? LW : 0) + (P - 2) * (DOPS + OPS);
   // dequantisation a step ahead (measured 2-6% on the 4-bit gs64 prefill
   // shapes; group size 32 would spill with it)
-  constexpr int IL = GS >= 64 ? KH_GEMM_IL : 0;
+  constexpr int IL = GS >= 64 && WR == 1 ? KH_GEMM_IL : 0;
   static_assert(WS0 + SC::OPS < 64, "vmcnt holds 6 bits");
   load_scales(0);
   __builtin_amdgcn_sched_barrier(0);
