@@ -334,6 +334,36 @@ bool gemv_path(const kh::QmvArgs& a) {
   return a.M <= kh::gemv_max_m(a.K, a.bits) && kh::gemv_fits(a.M, a.N, a.K, a.bits, a.gs);
 }
 
+// True when run_qmm takes the prefill GEMM for this call.
+bool gemm_path(const kh::QmvArgs& a, bool transpose) {
+  return fast_path(a, transpose) && !skinny_path(a) && !gemv_path(a) && kh::gemm_supported(a.K);
+}
+
+// The prefill GEMM for n parts that share x (M, K, bits, x dtype): the
+// activations are converted once, then each part's GEMM runs on them.
+// Results are those of n separate calls.
+int run_gemm_parts(const char* op, const kh::QmvArgs* a, int n) {
+  int rc;
+  const int64_t M = a[0].M, K = a[0].K;
+  size_t part = 0;
+  for (int i = 0; i < n; ++i) {
+    const kh::GemmPlan p = kh::plan_gemm((int)M, a[i].N, (int)K, a[i].bits);
+    part = std::max(part, kh::gemm_partial_bytes(p, (int)M, a[i].N));
+  }
+  // workspace: float16 activations | per-row scales | split-K partials
+  const size_t xb = (size_t)M * K * 2, rb = ((size_t)M * 4 + 255) / 256 * 256;
+  Workspace ws;
+  if (!workspace(a[0].stream, (xb + rb + part + 3) / 4, &ws, &rc, op)) return rc;
+  char* base = reinterpret_cast<char*>(ws.data);
+  float* rsc = reinterpret_cast<float*>(base + xb);
+  hipError_t e = kh::launch_prep_x(a[0], base, rsc);
+  for (int i = 0; i < n && e == hipSuccess; ++i) {
+    const kh::GemmPlan p = kh::plan_gemm((int)M, a[i].N, (int)K, a[i].bits);
+    e = kh::launch_gemm(a[i], p, base, rsc, reinterpret_cast<float*>(base + xb + rb));
+  }
+  return e == hipSuccess ? KH_OK : hip_fail(op, e);
+}
+
 // Kernel dispatch of one validated call.
 int run_qmm(const char* op, const kh::QmvArgs& a, bool transpose) {
   int rc;
@@ -349,17 +379,7 @@ int run_qmm(const char* op, const kh::QmvArgs& a, bool transpose) {
   } else if (gemv_path(a)) {
     e = kh::launch_gemv(a);
   } else if (kh::gemm_supported((int)K)) {
-    // workspace: float16 activations | per-row scales | split-K partials
-    const kh::GemmPlan p = kh::plan_gemm((int)M, (int)N, (int)K, a.bits);
-    const size_t xb = (size_t)M * K * 2, rb = ((size_t)M * 4 + 255) / 256 * 256;
-    const size_t bytes = xb + rb + kh::gemm_partial_bytes(p, (int)M, (int)N);
-    Workspace ws;
-    if (!workspace(st, (bytes + 3) / 4, &ws, &rc, op)) return rc;
-    char* base = reinterpret_cast<char*>(ws.data);
-    float* rsc = reinterpret_cast<float*>(base + xb);
-    e = kh::launch_prep_x(a, base, rsc);
-    if (e == hipSuccess)
-      e = kh::launch_gemm(a, p, base, rsc, reinterpret_cast<float*>(base + xb + rb));
+    return run_gemm_parts(op, &a, 1);
   } else if (M <= kh::kDecodeMaxM) {
     e = kh::launch_qmv(a);
   } else {
@@ -421,6 +441,9 @@ int kh_quantized_matmul_multi(int n, kh_array* const* res, const kh_array* x,
     const hipError_t e = kh::launch_gemv_multi(a.data(), n);
     return e == hipSuccess ? KH_OK : hip_fail(op, e);
   }
+  bool shared = true;  // every part on the prefill GEMM: convert x once
+  for (int i = 0; i < n && shared; ++i) shared = gemm_path(a[i], transpose);
+  if (shared) return run_gemm_parts(op, a.data(), n);
   for (int i = 0; i < n; ++i) {
     const int rc = run_qmm(op, a[i], transpose);
     if (rc) return rc;
@@ -457,8 +480,13 @@ int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gat
   char* ubuf = gbuf + (count * esz + 255) / 256 * 256;
   g.out = gbuf;
   u.out = ubuf;
-  if ((rc = run_qmm(op, g, true))) return rc;
-  if ((rc = run_qmm(op, u, true))) return rc;
+  if (gemm_path(g, true) && gemm_path(u, true)) {
+    const kh::QmvArgs gu[2] = {g, u};
+    if ((rc = run_gemm_parts(op, gu, 2))) return rc;
+  } else {
+    if ((rc = run_qmm(op, g, true))) return rc;
+    if ((rc = run_qmm(op, u, true))) return rc;
+  }
   const hipError_t e = kh::launch_silu_mul(gbuf, ubuf, res->data, res->dtype, (int64_t)count, g.stream);
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
 }

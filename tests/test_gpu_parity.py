@@ -343,7 +343,7 @@ def test_add_rejects_non_suffix_broadcast():
 
 # ----------------------------------------------------------------- fused neighbours (q/k/v, gate/up)
 
-@pytest.mark.parametrize("M", [1, 3, 8, 9, 40])
+@pytest.mark.parametrize("M", [1, 3, 8, 9, 40, 300])
 @pytest.mark.parametrize("bits,gs", [(4, 64), (8, 128)])
 def test_multi_equals_separate_calls(M, bits, gs):
     """kh_quantized_matmul_multi (the q/k/v triple on one x, nn.rs:724-726)
