@@ -371,13 +371,14 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
   constexpr int OPS = LW * NT;
   constexpr int BASE = OPS + (P - 2) * (DOPS + OPS);
   static_assert(BASE + SC::OPS < 64, "vmcnt holds 6 bits");
-  // Spread issue (128-row, 256-column tiles, one wave per SIMD): the loads
-  // of stage st + P - 1 are issued in four parts, part j
-  // (activation loads j*DOPS/4 .., code tile j) before MFMA step j of stage
-  // st, after the scale chunk when p == 0. The last activation load of a
-  // stage is then followed by its last code load and the P - 2 younger
-  // stages' loads, plus one scale chunk when one of those was issued at
-  // p == 0 (1 <= p <= P - 2).
+  // Spread issue (128- and 64-row tiles, one wave per SIMD): the loads of
+  // stage st + P - 1 are issued in four parts, part j (activation loads
+  // j*DOPS/4 .., code tile j) before MFMA step j of stage st, after the scale
+  // chunk when p == 0. The last activation load of a stage is then followed
+  // by its last code load and the P - 2 younger stages' loads, plus one scale
+  // chunk when one of those was issued at p == 0 (1 <= p <= P - 2). The
+  // prologue's stages go out in the plain order, which puts more ops after
+  // their last activation load: the same counts only wait longer there.
   constexpr bool SPREAD = KH_GEMM_SPREAD && (MT == 8 || (KH_GEMM_SPREAD4 && MT == 4)) &&
                           (NT == 4 || (KH_GEMM_SPREAD2 && NT == 2)) && WR == 1 && DOPS % 4 == 0;
   // (code tile j goes out in part j: with NT = 2 parts 2 and 3 carry none)

@@ -7,9 +7,9 @@
 // when T*k >= 64. Run pair by pair, every row streams its expert's whole
 // weight matrix; grouped, each expert's codes are read once per row tile.
 //
-//   1. the plan, over the whole GPU: group_count_kernel (one thread per
-//      pair) counts each workgroup's pairs per expert (ids outside [-E, E)
-//      form one more group); group_scan_kernel (one workgroup, one thread
+//   1. the plan, over the whole GPU: group_count_kernel (1024 pairs per
+//      workgroup) counts each workgroup's pairs per expert (ids outside
+//      [-E, E) form one more group) and marks every padded row as padding; group_scan_kernel (one workgroup, one thread
 //      per group) pads each group's rows to whole m-tiles of 16*mt rows,
 //      writes the expert of every m-tile and turns the counts into each
 //      workgroup's first slot per group; group_pos_kernel (the count
