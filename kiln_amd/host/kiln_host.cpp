@@ -232,6 +232,15 @@ Array Array::share() const {
   return a;
 }
 
+Result<Array> Array::view(const std::vector<int64_t>& shape) const {
+  int64_t n = 1;
+  for (int64_t d : shape) n *= d;
+  if (n != size()) return Error{"[view] shape does not hold the same number of elements"};
+  Array a = share();
+  a.shape_ = shape;
+  return a;
+}
+
 Result<std::vector<uint8_t>> Array::to_bytes(const Stream& s) const {
   std::vector<uint8_t> out(nbytes());
   if (!out.empty()) {
@@ -278,6 +287,54 @@ Result<Array> quantized_matmul(const Array& x, const Array& w, const Array& scal
   const int st = kh_quantized_matmul(&res, &xd, &wd, &sd, &bd, transpose, opt(group_size), opt(bits),
                                      "affine", s.raw());
   if (st) return kh_error(st);
+  return out;
+}
+
+Result<Array> gather_qmm(const Array& x, const Array& w, const Array& scales, const Array& biases,
+                         const Array& indices, bool transpose, int group_size, int bits,
+                         bool sorted_indices, const Stream& s) {
+  if (x.ndim() < 2 || w.ndim() != 3)
+    return Error{"[gather_qmm] x must be [..., M, K] and w an expert stack [E, N, K*bits/32]"};
+  if (!transpose) return Error{"[gather_qmm] transpose=false is not supported (Kiln passes true)"};
+  // batch = broadcast(x.shape[:-2], indices.shape), numpy rules
+  const int xb = x.ndim() - 2, ib = indices.ndim(), nd = std::max(xb, ib);
+  std::vector<int64_t> shape(nd);
+  for (int d = 0; d < nd; ++d) {
+    const int dx = d - (nd - xb), di = d - (nd - ib);
+    const int64_t sx = dx >= 0 ? x.dim(dx) : 1, si = di >= 0 ? indices.dim(di) : 1;
+    if (sx != si && sx != 1 && si != 1) return Error{"[gather_qmm] x and indices do not broadcast"};
+    shape[d] = sx == 1 ? si : sx;
+  }
+  shape.push_back(x.dim(-2));
+  shape.push_back(w.dim(1));
+  auto r = Array::empty(shape, promote(x.dtype(), scales.dtype()), s);
+  if (!r) return r;
+  Array out = r.take();
+  kh_array res = out.desc(), xd = x.desc(), wd = w.desc(), sd = scales.desc(), bd = biases.desc(),
+           id = indices.desc();
+  const int st = kh_gather_qmm(&res, &xd, &wd, &sd, &bd, &id, transpose, opt(group_size), opt(bits), "affine",
+                               sorted_indices, s.raw());
+  if (st) return kh_error(st);
+  return out;
+}
+
+Result<Array> stack(const std::vector<Array>& parts, const Stream& s) {
+  if (parts.empty()) return Error{"[stack] no arrays to stack"};
+  for (const Array& p : parts)
+    if (p.shape() != parts[0].shape() || p.dtype() != parts[0].dtype())
+      return Error{"[stack] arrays differ in shape or dtype"};
+  std::vector<int64_t> shape = parts[0].shape();
+  shape.insert(shape.begin(), (int64_t)parts.size());
+  auto r = Array::empty(shape, parts[0].dtype(), s);
+  if (!r) return r;
+  Array out = r.take();
+  const size_t each = parts[0].nbytes();
+  for (size_t i = 0; i < parts.size(); ++i) {
+    if (each == 0) break;
+    const hipError_t e = hipMemcpyAsync(static_cast<char*>(out.data()) + i * each, parts[i].data(), each,
+                                        hipMemcpyDeviceToDevice, s.raw());
+    if (e != hipSuccess) return Error{std::string("[stack] ") + hipGetErrorString(e)};
+  }
   return out;
 }
 
@@ -537,6 +594,70 @@ Result<Array> Linear::forward(const Array& x, const Stream& s) const {
 std::pair<int64_t, int64_t> Linear::io_features() const {
   if (quantized_) return {scales_.dim(1) * group_size_, scales_.dim(0)};
   return {weight_.dim(1), weight_.dim(0)};
+}
+
+Result<SwitchLinear> SwitchLinear::load(WeightStore& store, const std::string& mlp_prefix,
+                                        const std::string& proj, int num_experts,
+                                        const std::optional<Quantization>& q, const Stream& s) {
+  const std::string stacked = mlp_prefix + ".switch_mlp." + proj;
+  auto per = [&](int e, const char* name) {
+    return mlp_prefix + ".experts." + std::to_string(e) + "." + proj + "." + name;
+  };
+  const bool is_stacked = store.contains(stacked + ".scales");
+  if (!is_stacked && !store.contains(per(0, "scales")))
+    return Error{"dense " + stacked + " is outside the quantized path this library implements"};
+  if (!q)
+    return Error{"weights/config mismatch: " + stacked +
+                 " has quantized tensors but config.json has no quantization block"};
+  if (num_experts < 1) return Error{"[SwitchLinear] num_experts must be >= 1"};
+  // one tensor of every expert, stacked along axis 0
+  auto gather = [&](const char* name) -> Result<Array> {
+    std::vector<Array> parts;
+    for (int e = 0; e < num_experts; ++e) {
+      auto t = store.take(per(e, name));
+      if (!t) return t.error();
+      parts.push_back(t.take());
+    }
+    return ops::stack(parts, s);
+  };
+  auto one = [&](const char* name) -> Result<Array> {
+    return is_stacked ? store.take(stacked + "." + name) : gather(name);
+  };
+  SwitchLinear l;
+  auto w = one("weight");
+  if (!w) return w.error();
+  auto sc = one("scales");
+  if (!sc) return sc.error();
+  auto bi = one("biases");
+  if (!bi) return bi.error();
+  l.weight_ = w.take();
+  l.scales_ = sc.take();
+  l.biases_ = bi.take();
+  if (l.weight_.ndim() != 3 || l.weight_.dim(0) != num_experts)
+    return Error{"[SwitchLinear] " + stacked + ".weight is not a stack of " + std::to_string(num_experts) +
+                 " experts"};
+  if (is_stacked ? store.contains(stacked + ".bias") : store.contains(per(0, "bias"))) {
+    auto b = one("bias");
+    if (!b) return b.error();
+    l.bias_ = b.take();
+  }
+  l.group_size_ = q->group_size;
+  l.bits_ = q->bits;
+  return l;
+}
+
+Result<Array> SwitchLinear::forward(const Array& x, const Array& indices, bool sorted_indices,
+                                    const Stream& s) const {
+  auto y = ops::gather_qmm(x, weight_, scales_, biases_, indices, true, group_size_, bits_, sorted_indices, s);
+  if (!y || !bias_) return y;
+  // y + expand_dims(bias[indices], -2): bias rows gathered to indices.shape + [N]
+  if (y.value().dim(-2) != 1 || y.value().ndim() != indices.ndim() + 2)
+    return Error{"[SwitchLinear] an expert bias needs one row per batch pair"};
+  auto g = ops::take(*bias_, indices, 0, s);
+  if (!g) return g;
+  auto gv = g.value().view(y.value().shape());
+  if (!gv) return gv.error();
+  return ops::add(y.value(), gv.value(), s);
 }
 
 Result<Embedding> Embedding::load(WeightStore& store, const std::string& prefix,

@@ -3,10 +3,11 @@
 // Mirrors, for the quantized-linear path, the Rust surface Kiln's models are
 // written against, so that layer code ports one-to-one:
 //   kiln::Array / Stream / Error / Result   crates/kiln-mlx/src/{array,stream,error}.rs
-//   kiln::ops::{quantized_matmul, dequantize, take, add}   crates/kiln-mlx/src/ops.rs
+//   kiln::ops::{quantized_matmul, gather_qmm, dequantize, take, add}   crates/kiln-mlx/src/ops.rs
 //   kiln::WeightStore                      crates/kiln-models/src/weights.rs:37-130
 //   kiln::Quantization, validate_*         crates/kiln-models/src/config.rs:28-33, 137-148, 735-760
 //   kiln::nn::Linear / Embedding           crates/kiln-models/src/nn.rs:30-194
+//   kiln::nn::SwitchLinear                 crates/kiln-models/src/moe.rs:47-176
 //   kiln::nn::probe_row_stability          crates/kiln-models/src/nn.rs:301-327
 //
 // Conventions carried over: fallible calls return Result (never abort); an
@@ -120,6 +121,9 @@ class Array {
                                   Dtype dtype, const Stream& s);
   // A non-owning alias of the same buffer (MLX Clone aliases too).
   Array share() const;
+  // A non-owning alias with another shape of the same element count (a
+  // reshape of a row-contiguous array).
+  Result<Array> view(const std::vector<int64_t>& shape) const;
 
   Result<std::vector<uint8_t>> to_bytes(const Stream& s) const;  // synchronises `s`
   int ndim() const { return (int)shape_.size(); }
@@ -154,6 +158,14 @@ namespace ops {
 Result<Array> quantized_matmul(const Array& x, const Array& w, const Array& scales,
                                const Array& biases, bool transpose, int group_size, int bits,
                                const Stream& s);
+// ops.rs:390-429 with null lhs_indices: per batch pair, x[b] @ w[e_b]^T over
+// expert stacks w/scales/biases [E, N, ..]; batch = broadcast(x.shape[:-2],
+// indices.shape); result [batch..., M, N].
+Result<Array> gather_qmm(const Array& x, const Array& w, const Array& scales, const Array& biases,
+                         const Array& indices, bool transpose, int group_size, int bits,
+                         bool sorted_indices, const Stream& s);
+// Arrays of one shape and dtype stacked along a new axis 0 (mx.stack).
+Result<Array> stack(const std::vector<Array>& parts, const Stream& s);
 // ops.rs:456-484 (output dtype = scales dtype).
 Result<Array> dequantize(const Array& w, const Array& scales, const Array& biases, int group_size,
                          int bits, const Stream& s);
@@ -223,6 +235,27 @@ class Embedding {
  private:
   bool quantized_ = false;
   Array weight_, scales_, biases_;
+  int group_size_ = 64, bits_ = 4;
+};
+
+// SwitchLinear (moe.rs:47-176), quantized form: one projection per expert,
+// stacked [E, out, in], applied with gather_qmm on per-token expert ids.
+// Loads `{mlp_prefix}.switch_mlp.{proj}` (already stacked, as mlx-lm saves
+// after conversion) or `{mlp_prefix}.experts.{e}.{proj}` (stacked here along
+// axis 0, as the reference's load does).
+class SwitchLinear {
+ public:
+  static Result<SwitchLinear> load(WeightStore& store, const std::string& mlp_prefix, const std::string& proj,
+                                   int num_experts, const std::optional<Quantization>& q, const Stream& s);
+  // x @ W[indices]^T (+ bias[indices]); sorted_indices is the caller's
+  // do_sort (a scheduling hint, moe.rs:124-176). With an expert bias, each
+  // batch pair must hold one row (SwitchGlu's use).
+  Result<Array> forward(const Array& x, const Array& indices, bool sorted_indices, const Stream& s) const;
+  int num_experts() const { return (int)weight_.dim(0); }
+
+ private:
+  Array weight_, scales_, biases_;
+  std::optional<Array> bias_;
   int group_size_ = 64, bits_ = 4;
 };
 

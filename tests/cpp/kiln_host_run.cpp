@@ -139,7 +139,18 @@ static int job(const std::string& path) {
   if (!x) return fail_json(x.error().message);
 
   Result<Array> y = Error{"unknown op " + op};
-  if (op == "linear") {
+  if (op == "switch") {  // SwitchLinear: prefix = the MLP prefix, plus proj, experts, ids
+    std::vector<int64_t> ishape;
+    for (const auto& d : j.get("ids_shape")->arr) ishape.push_back((int64_t)d.num);
+    std::ifstream idf(j.get("ids")->str, std::ios::binary);
+    std::string ib((std::istreambuf_iterator<char>(idf)), std::istreambuf_iterator<char>());
+    auto ids = Array::from_bytes(ib.data(), ib.size(), ishape, Dtype::Uint32, s);
+    if (!ids) return fail_json(ids.error().message);
+    auto sl = nn::SwitchLinear::load(store.value(), prefix, j.get("proj")->str, (int)j.get("experts")->num,
+                                     quant.value(), s);
+    if (!sl) return fail_json(sl.error().message);
+    y = sl.value().forward(x.value(), ids.value(), j.get("sorted") && j.get("sorted")->b, s);
+  } else if (op == "linear") {
     auto l = nn::Linear::load(store.value(), prefix, quant.value());
     if (!l) return fail_json(l.error().message);
     y = l.value().forward(x.value(), s);

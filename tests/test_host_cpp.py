@@ -133,3 +133,52 @@ def test_missing_quantization_block_is_an_error(tmp_path):
     rc, out, err = _job(tmp_path, model_dir=str(d), op="load", prefix="model.layers.0.mlp.gate_proj")
     assert rc == 2 and not out["ok"]
     assert "no quantization block" in out["error"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("form", ["per_expert", "stacked"])
+@pytest.mark.parametrize("P", [6, 80])
+def test_switch_linear_from_checkpoint(oracle, tmp_path, form, P):
+    """nn::SwitchLinear (moe.rs:47-176): experts stacked at load from
+    `experts.{e}.{proj}` or taken as `switch_mlp.{proj}`, then x @ W[ids]^T
+    (+ bias[ids]) through gather_qmm; each row against the oracle on its
+    expert. P = 6 pairs run pair by pair, P = 80 through the grouped GEMM."""
+    from safetensors.numpy import save_file
+    E, N, K, gs = 4, 48, 256, 64
+    Ls = [make_linear_numpy(N, K, gs, "q4", seed=60 + e) for e in range(E)]
+    bias = (np.random.default_rng(61).standard_normal((E, N)) * 0.1).astype(np.float16)
+    pre = "model.layers.0.mlp"
+    t = {}
+    if form == "stacked":
+        t[f"{pre}.switch_mlp.up_proj.weight"] = np.stack([L["w"] for L in Ls])
+        t[f"{pre}.switch_mlp.up_proj.scales"] = np.stack([L["scales"] for L in Ls]).view(np.float16)
+        t[f"{pre}.switch_mlp.up_proj.biases"] = np.stack([L["biases"] for L in Ls]).view(np.float16)
+        t[f"{pre}.switch_mlp.up_proj.bias"] = bias
+    else:
+        for e, L in enumerate(Ls):
+            t[f"{pre}.experts.{e}.up_proj.weight"] = L["w"]
+            t[f"{pre}.experts.{e}.up_proj.scales"] = L["scales"].view(np.float16)
+            t[f"{pre}.experts.{e}.up_proj.biases"] = L["biases"].view(np.float16)
+            t[f"{pre}.experts.{e}.up_proj.bias"] = bias[e]
+    d = tmp_path / form
+    d.mkdir()
+    save_file(t, str(d / "model.safetensors"))
+    (d / "config.json").write_text(json.dumps({"model_type": "olmoe",
+                                               "quantization": {"group_size": gs, "bits": 4}}))
+    ids = np.sort(np.random.default_rng(62).integers(0, E, P)).astype(np.uint32)
+    x = make_x_numpy(P, K, seed=63, xdt="f16")
+    (tmp_path / "x.bin").write_bytes(x.tobytes())
+    (tmp_path / "ids.bin").write_bytes(ids.tobytes())
+    rc, out, err = _job(tmp_path, model_dir=str(d), op="switch", prefix=pre, proj="up_proj", experts=E,
+                        input=str(tmp_path / "x.bin"), input_shape=[P, 1, K], input_dtype="float16",
+                        ids=str(tmp_path / "ids.bin"), ids_shape=[P], sorted=True,
+                        output=str(tmp_path / "y.bin"))
+    assert rc == 0 and out["ok"], (out, err)
+    assert out["shape"] == [P, 1, N] and out["dtype"] == "float16"
+    y = np.frombuffer((tmp_path / "y.bin").read_bytes(), dtype=np.float16).astype(np.float64).reshape(P, N)
+    for p in range(P):
+        e = int(ids[p])
+        r16 = oracle.quantized_matmul(x[p:p + 1], "f16", Ls[e]["w"], Ls[e]["scales"], Ls[e]["biases"], "f16",
+                                      gs, 4, True, "f16")
+        ref = (oracle.to_f32(r16, "f16") + bias[e].astype(np.float32)).astype(np.float16).astype(np.float64)[0]
+        assert np.max(np.abs(y[p] - ref)) <= 2e-2 * np.max(np.abs(ref)), p
