@@ -55,7 +55,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--profile", choices=["decode", "prefill", "traffic", "moe"], default=None,
+    ap.add_argument("--profile", choices=["decode", "decode8", "prefill", "traffic", "moe"], default=None,
                     help="run one workload for a profiler and exit (no JSON line): the M=1 decode "
                          "step, the M=2048 Llama-3-8B layer, or a copy of known size followed by "
                          "gate-shape GEMV launches (counter calibration)")
@@ -193,6 +193,11 @@ def profile_run(kind, torch, ops, layers, shapes, layer_fns, dev, gs, bits):
     """Workloads for rocprofv3 (kernel trace or counters), eager launches."""
     if kind == "decode":
         step, _ = layer_fns(layers, shapes, 1, gs, bits)
+        for r in range(4 * len(layers)):
+            step(r % len(layers))
+    elif kind == "decode8":
+        # small-batch decode: the 7 linears at M = 8 over the rotated copies
+        step, _ = layer_fns(layers, shapes, 8, gs, bits)
         for r in range(4 * len(layers)):
             step(r % len(layers))
     elif kind == "prefill":
