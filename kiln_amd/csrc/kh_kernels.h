@@ -25,6 +25,9 @@ struct QmvArgs {
 // M rows on the matrix cores, exact products (kh_skinny.hip).
 constexpr int kSkinnyMaxM = 32;
 bool skinny_supported(int64_t M, int64_t N, int64_t K, int bits, int gs);
+// Waves of the skinny launch with one 16-row tile per workgroup: ceil(N/16)
+// times the waves that split K (the largest divisor of K/128 up to 8).
+int64_t skinny_waves(int64_t N, int64_t K);
 hipError_t launch_skinny(const QmvArgs& a);
 
 // Largest M served by the decode kernel; larger M takes the prefill GEMM.

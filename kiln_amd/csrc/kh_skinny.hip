@@ -308,6 +308,13 @@ hipError_t launch_b(const QmvArgs& a, const SkinnyPlan& p) {
 
 }  // namespace
 
+int64_t skinny_waves(int64_t N, int64_t K) {
+  const int np = (int)(K / kPiece);
+  int W = kSkMaxWaves;
+  while (W > 1 && np % W) --W;
+  return (N + 15) / 16 * W;
+}
+
 bool skinny_supported(int64_t M, int64_t N, int64_t K, int bits, int gs) {
   const int64_t lim = (int64_t)1 << 31;
   if (!(M >= 1 && M <= kSkinnyMaxM && K % kPiece == 0 && N >= 1 && N * K * bits / 8 < lim &&

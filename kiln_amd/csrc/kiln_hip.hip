@@ -321,8 +321,16 @@ bool fast_path(const kh::QmvArgs& a, bool transpose) {
 #ifndef KH_SKINNY_MIN_M
 #define KH_SKINNY_MIN_M 5  // smallest M the skinny MFMA kernel takes over from the GEMV (measured)
 #endif
+#ifndef KH_SKINNY_MIN_WAVES
+#define KH_SKINNY_MIN_WAVES 1024  // narrower skinny launches leave the GEMV the M it serves (measured)
+#endif
 bool skinny_path(const kh::QmvArgs& a) {
-  return a.M >= KH_SKINNY_MIN_M && kh::skinny_supported(a.M, a.N, a.K, a.bits, a.gs);
+  if (a.M < KH_SKINNY_MIN_M || !kh::skinny_supported(a.M, a.N, a.K, a.bits, a.gs)) return false;
+  // Narrow shapes (k/v 1024x4096: 64 workgroups, 512 waves) fill the chip
+  // better through the decode GEMV up to its M limit (7.4 -> 6.3 us at
+  // M = 8); a rule on N and K, so rows stay M-invariant within each kernel.
+  return !(a.M <= kh::gemv_max_m(a.K, a.bits) && kh::gemv_fits(a.M, a.N, a.K, a.bits, a.gs) &&
+           kh::skinny_waves(a.N, a.K) < KH_SKINNY_MIN_WAVES);
 }
 #ifndef KH_GROUP_MIN_ROWS
 #define KH_GROUP_MIN_ROWS 64  // gather_qmm: fewest rows (pairs * M) for the grouped GEMM

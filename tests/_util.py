@@ -48,24 +48,29 @@ def gemv_max_m(K: int, bits: int) -> int:
     return 8 if I == 1 else 2 if I == 2 else 1 if I <= 4 else 0
 
 
-def skinny_fits(M: int, N: int, K: int) -> bool:
-    """The skinny MFMA kernel's own range rule (kh_skinny.hip): K % 128 == 0,
-    5 <= M <= 32, and above 16 rows only where ceil(N/16) * W waves fit one
-    round (W = the largest divisor of K/128 up to 8)."""
+def skinny_fits(M: int, N: int, K: int, bits: int = 4) -> bool:
+    """The skinny MFMA kernel's range rule (kh_skinny.hip, skinny_path in
+    kiln_hip.hip): K % 128 == 0, 5 <= M <= 32; not where its launch has
+    fewer than 1024 waves (ceil(N/16) * W, W = the largest divisor of K/128
+    up to 8) and the decode GEMV takes M; above 16 rows only where those
+    waves fit one round."""
     if K % 128 or not 5 <= M <= 32:
+        return False
+    np_ = K // 128
+    W = max(w for w in range(1, 9) if np_ % w == 0)
+    waves = -(-N // 16) * W
+    if M <= gemv_max_m(K, bits) and waves < 1024:
         return False
     if M <= 16:
         return True
-    np_ = K // 128
-    W = max(w for w in range(1, 9) if np_ % w == 0)
-    return -(-N // 16) * W <= 3 * 4 * 256
+    return waves <= 3 * 4 * 256
 
 
 def decode_regime(M: int, K: int, bits: int, N: int):
     """Which kernel (and tiling class) kh_quantized_matmul uses for a
     transpose=true call with bf16/f16 x and 16-bit scales: rows of the result
     are bitwise identical for every M of one regime (kiln_hip.hip, run_qmm)."""
-    if skinny_fits(M, N, K):
+    if skinny_fits(M, N, K, bits):
         return ("skinny",)
     if M <= gemv_max_m(K, bits):
         return ("gemv",)

@@ -706,11 +706,13 @@ def test_skinny_kernel_exact(oracle, bits, gs, xdt):
     """The small-batch MFMA kernel (5 <= M <= 32, K % 128 == 0) keeps every
     dequantised weight exact: ragged N, one piece (K = 128, one wave), odd
     piece counts per wave (K = 896), one and two m-tiles, the 8-bit bf16
-    nibble-split operands."""
-    for N, K in ((37, 128), (272, 896), (50, 4096)):
-        for M in (5, 13, 16, 17, 32):
-            print(f"case skinny bits={bits} gs={gs} xdt={xdt} N={N} K={K} M={M}", flush=True)
-            assert decode_regime(M, K, bits, N)[0] == "skinny"
-            L, x = _case(M, N, K, gs, bits, xdt=xdt, seed=M + N + K + bits)
-            y = _run(L, x, gs, bits, xdt, "f16", "f32")
-            _check_f32(oracle, L, x, gs, bits, xdt, "f16", y, rel=EXACT_REL)
+    nibble-split operands. Narrow shapes take it from M = 9 (below, the
+    decode GEMV fills the chip better); M = 5 and 8 run on wide ones."""
+    cases = [(N, K, M) for N, K in ((37, 128), (272, 896), (50, 4096)) for M in (13, 16, 17, 32)]
+    cases += [(N, K, M) for N, K in ((16390, 128), (2360, 896), (2050, 4096)) for M in (5, 8)]
+    for N, K, M in cases:
+        print(f"case skinny bits={bits} gs={gs} xdt={xdt} N={N} K={K} M={M}", flush=True)
+        assert decode_regime(M, K, bits, N)[0] == "skinny"
+        L, x = _case(M, N, K, gs, bits, xdt=xdt, seed=M + N + K + bits)
+        y = _run(L, x, gs, bits, xdt, "f16", "f32")
+        _check_f32(oracle, L, x, gs, bits, xdt, "f16", y, rel=EXACT_REL)
