@@ -23,7 +23,10 @@
 //     instruction four whole rows, 1 KB contiguous), into a ring of LDS
 //     buffers, row-major with the 16-byte blocks XOR-swizzled by row so the
 //     MFMA operand reads are free of bank conflicts;
-//   - one barrier per stage.
+//   - one barrier per stage; a stage's loads go out in four parts, one
+//     before each MFMA step of the stage three earlier (one wave per SIMD
+//     would otherwise stall at issue with the matrix core idle), and the
+//     weights of MFMA step j+1 are dequantised between the MFMAs of step j.
 // K slices (split-K, chosen from N, K and M-tiles only) write float32
 // partials that gemm_reduce sums in slice order, so results are
 // deterministic. Tiles are ordered in bands of 4 m-tiles (m fastest within a
