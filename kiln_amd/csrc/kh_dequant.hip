@@ -71,28 +71,39 @@ __device__ __forceinline__ int64_t resolve_id(const void* ids, bool ids_signed, 
   return (id < 0 || id >= V) ? -1 : id;
 }
 
-template <int BITS, bool VEC>
+// WPT = 2: a thread expands two consecutive words of a row (one 8-byte load,
+// both in one group since gs >= 32 codes) and stores them back to back.
+template <int BITS, bool VEC, int WPT>
 __global__ void embedding_kernel(const void* __restrict__ ids, int ids_signed, int64_t T,
                                  const uint32_t* __restrict__ w, const void* __restrict__ scales,
                                  const void* __restrict__ biases, int sdt, void* __restrict__ out,
                                  int odt, int64_t V, int64_t H, int gs) {
   constexpr int CPW = 32 / BITS;
-  const int64_t WR = H / CPW;
+  const int64_t WR = H / CPW, UR = WR / WPT;  // words and thread units per row
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= T * WR) return;
-  const int64_t t = i / WR, wi = i % WR;
+  if (i >= T * UR) return;
+  const int64_t t = i / UR, wi = (i % UR) * WPT;
   const int64_t id = resolve_id(ids, ids_signed != 0, t, V);
-  float v[CPW];
+  float v[WPT][CPW];
   if (id < 0) {
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) v[c] = 0.f;
+    for (int k = 0; k < WPT; ++k)
+#pragma unroll
+      for (int c = 0; c < CPW; ++c) v[k][c] = 0.f;
   } else {
     const int64_t G = H / gs;
     const int64_t si = id * G + (wi * CPW) / gs;
-    expand_word<BITS>(w[id * WR + wi], load_as_f32(scales, sdt, si), load_as_f32(biases, sdt, si),
-                      v);
+    const float sc = load_as_f32(scales, sdt, si), bi = load_as_f32(biases, sdt, si);
+    if constexpr (WPT == 2) {
+      const u32x2 q = *reinterpret_cast<const u32x2*>(w + id * WR + wi);
+      expand_word<BITS>(q[0], sc, bi, v[0]);
+      expand_word<BITS>(q[1], sc, bi, v[1]);
+    } else {
+      expand_word<BITS>(w[id * WR + wi], sc, bi, v[0]);
+    }
   }
-  store_codes<CPW, VEC>(out, odt, t * H + wi * CPW, v);
+#pragma unroll
+  for (int k = 0; k < WPT; ++k) store_codes<CPW, VEC>(out, odt, t * H + (wi + k) * CPW, v[k]);
 }
 
 // take on rows of `units` elements of type U.
@@ -328,16 +339,20 @@ hipError_t launch_embedding(const void* ids, bool ids_signed, int64_t T, const v
   const int64_t words = T * (H * bits / 32);
   if (words == 0) return hipSuccess;
   const bool vec = (reinterpret_cast<uintptr_t>(out) % 16) == 0;
-  const dim3 grid(blocks_for(words, 256)), block(256);
   const uint32_t* wp = static_cast<const uint32_t*>(w);
   const int sg = ids_signed ? 1 : 0;
+  const dim3 block(256);
+  // two words per thread where rows hold an even number of 8-byte aligned words
+  const bool two = vec && ((H * bits / 32) % 2) == 0 && (reinterpret_cast<uintptr_t>(w) % 8) == 0;
+#define KH_EMB(B, VC, P)                                                                                 \
+  hipLaunchKernelGGL((embedding_kernel<B, VC, P>), dim3(blocks_for(words / P, 256)), block, 0, stream, ids, \
+                     sg, T, wp, scales, biases, sdt, out, odt, V, H, gs)
   if (bits == 4) {
-    if (vec) hipLaunchKernelGGL((embedding_kernel<4, true>), grid, block, 0, stream, ids, sg, T, wp, scales, biases, sdt, out, odt, V, H, gs);
-    else hipLaunchKernelGGL((embedding_kernel<4, false>), grid, block, 0, stream, ids, sg, T, wp, scales, biases, sdt, out, odt, V, H, gs);
+    if (two) KH_EMB(4, true, 2); else if (vec) KH_EMB(4, true, 1); else KH_EMB(4, false, 1);
   } else {
-    if (vec) hipLaunchKernelGGL((embedding_kernel<8, true>), grid, block, 0, stream, ids, sg, T, wp, scales, biases, sdt, out, odt, V, H, gs);
-    else hipLaunchKernelGGL((embedding_kernel<8, false>), grid, block, 0, stream, ids, sg, T, wp, scales, biases, sdt, out, odt, V, H, gs);
+    if (two) KH_EMB(8, true, 2); else if (vec) KH_EMB(8, true, 1); else KH_EMB(8, false, 1);
   }
+#undef KH_EMB
   return hipGetLastError();
 }
 
