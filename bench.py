@@ -60,6 +60,8 @@ def main():
                          "step, the M=2048 Llama-3-8B layer, or a copy of known size followed by "
                          "gate-shape GEMV launches (counter calibration)")
     args = ap.parse_args()
+    if args.steps < 1 or args.warmup < 0:
+        ap.error("--steps must be >= 1 and --warmup >= 0")
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build runs the quantized linear path on a "
               f"single MI355X and has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -133,11 +135,8 @@ def main():
         profile_run(args.profile, torch, ops, layers, shapes, layer_fns, dev, gs, bits)
         return
     step, per = layer_fns(layers, shapes, 1, gs, bits)
-    reps = max(1, -(-args.steps // copies))
-    wreps = max(1, -(-args.warmup // copies))
-    graph_us(step, copies, wreps)  # warm-up
-    step_us = graph_us(step, copies, reps)
-    nsteps = reps * copies
+    step_us = timed_steps_us(torch, step, copies, args.steps, args.warmup, stream)
+    nsteps = args.steps
     step_bytes = sum(call_bytes(N, K, 1, bits, gs) for _, N, K in shapes)
     value = step_bytes / (step_us * 1e-6) / 1e9
     per_shape_us = {name: graph_us(per[name], copies, 20) for name, _, _ in shapes}
@@ -146,6 +145,8 @@ def main():
     dom_bytes = call_bytes(dN, dK, 1, bits, gs)
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
 
+    reps = max(1, -(-args.steps // copies))
+    rot_us = graph_us(step, copies, reps)  # the same step, one graph of `copies` steps replayed
     fused = fused_step(torch, ops, layers, shapes, graph_us, dev, g, gs, bits, copies, reps)
 
     sweep = {} if args.no_sweep else run_sweep(torch, ops, layers, shapes, graph_us, layer_fns,
@@ -159,7 +160,7 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": nsteps,
-        "warmup": wreps * copies,
+        "warmup": args.warmup,
         "ms_per_step": round(step_us * 1e-3, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -174,10 +175,14 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      # HBM bytes per gate launch, FETCH_SIZE + WRITE_SIZE scaled by
-                     # what they read for a 256 MiB copy (x1.99976 and x1.0)
+                     # what they read for a 256 MiB copy (x1.99976 and x1.0), from
+                     # the `--profile traffic` runs summarised in profiles/
                      "traffic": GATE_TRAFFIC_BYTES,
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of bench.py --profile "
+                                       "traffic (profiles/gemv_traffic_llama3-8b_gate_m1.md)",
                      "kernel": "gemv_kernel<4,bf16,f16,M=1,R=4,I=1> at gate 14336x4096",
                      "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 3)},
+        "step_us_rotating_graph": round(rot_us, 3),
         "per_shape_us": {k: round(v, 2) for k, v in per_shape_us.items()},
         "per_shape_gbs": {n: round(call_bytes(N, K, 1, bits, gs) / (per_shape_us[n] * 1e-6) / 1e9, 1)
                           for n, N, K in shapes},
@@ -187,6 +192,37 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def timed_steps_us(torch, step, copies, steps, warmup, stream):
+    """Average µs per step over exactly `steps` decode steps, after exactly
+    `warmup` untimed ones. Each run is one HIP graph holding that many steps,
+    step i on weight copy i % copies; HIP events on the replay stream, with a
+    device synchronisation on both sides of the timed replay."""
+    for c in range(copies):  # eager once per copy: every plan's workspace exists
+        step(c)
+    torch.cuda.synchronize()
+
+    def capture(n):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(n):
+                step(i % copies)
+        return graph
+
+    timed = capture(steps)
+    if warmup:
+        warm = capture(warmup)
+        warm.replay()
+        del warm
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    timed.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return 1e3 * e0.elapsed_time(e1) / steps
 
 
 def profile_run(kind, torch, ops, layers, shapes, layer_fns, dev, gs, bits):

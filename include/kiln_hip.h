@@ -215,6 +215,14 @@ int kh_quantized_embedding(kh_array* res, const kh_array* ids,
  * res has a's shape. Each sum is formed in float32 and rounded once to res. */
 int kh_add(kh_array* res, const kh_array* a, const kh_array* b, kh_stream stream);
 
+/* Diagnostics, no counterpart in the reference: writes to buf the name of the
+ * kernel plan kh_quantized_matmul runs for a transpose=true call of this
+ * shape and these dtypes with 16-byte aligned operands ("gemv", "skinny",
+ * "gemm mt=.. nsplit=.. tail=..", "qmv", "qmm" or "generic"). For tests and
+ * profiling tools that need to know which kernel a shape exercises. */
+int kh_quantized_matmul_plan(int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                             int x_dtype, int scales_dtype, char* buf, size_t len);
+
 /* Message of the last failing call on this thread ("" if none). */
 const char* kh_last_error(void);
 

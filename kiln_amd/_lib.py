@@ -24,7 +24,7 @@ STATUS = {0: "KH_OK", 1: "KH_ERR_INVALID_ARGUMENT", 2: "KH_ERR_UNSUPPORTED",
 EXPORTS = ("kh_quantized_matmul", "kh_quantized_matmul_multi", "kh_quantized_gate_up",
            "kh_gather_qmm", "kh_quantize",
            "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add", "kh_last_error",
-           "kh_version")
+           "kh_version", "kh_quantized_matmul_plan")
 
 
 class KhArray(ctypes.Structure):
@@ -77,6 +77,10 @@ def lib() -> ctypes.CDLL:
                   "kh_gather_qmm", "kh_quantize",
                   "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add"):
             getattr(L, f).restype = ctypes.c_int
+        L.kh_quantized_matmul_plan.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                               ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_char_p, ctypes.c_size_t]
+        L.kh_quantized_matmul_plan.restype = ctypes.c_int
         L.kh_last_error.restype = ctypes.c_char_p
         L.kh_version.restype = ctypes.c_char_p
         _lib = L

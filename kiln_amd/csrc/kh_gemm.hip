@@ -127,46 +127,11 @@ __device__ __forceinline__ int step_off(int j, int lg) {
 // Stages kept in flight (measured on the Llama-3-8B shapes): 4 for the
 // smallest tiles (latency-bound launches) and the largest (one wave per SIMD:
 // the ring is what hides memory latency), 2 at 64 rows.
-#ifndef KH_GEMM_NT
-#define KH_GEMM_NT 0  // code loads marked non-temporal (measured: 3-7% slower: the codes of
-                      // a column tile are re-read by every row tile and now stay cached)
-#endif
-#ifndef KH_GEMM_GM
-#define KH_GEMM_GM 4  // m-tiles per band of the tile order (1 = n fastest; 4 measured best)
-#endif
-#ifndef KH_GEMM_CAP
-#define KH_GEMM_CAP 256  // split-K target: workgroups per launch (one per CU)
-#endif
-#ifndef KH_GEMM_TAIL
-#define KH_GEMM_TAIL 1  // run a partial last round of 128-row tiles as half-width workgroups
-#endif
-#ifndef KH_GEMM_SPREAD
-#define KH_GEMM_SPREAD 1  // issue each stage's loads spread over the MFMA steps (128-row tiles)
-#endif
-#ifndef KH_GEMM_SPREAD2
-#define KH_GEMM_SPREAD2 1  // ... also for the half-width tail workgroups
-#endif
-#ifndef KH_GEMM_SPREAD4
-#define KH_GEMM_SPREAD4 1  // ... also for 64-row tiles
-#endif
-#ifndef KH_GEMM_IL
-#define KH_GEMM_IL 2  // VALU ops scheduled after each MFMA when dequantising a step ahead (0: off)
-#endif
-#ifndef KH_GEMM_P
-#define KH_GEMM_P 0   // tuning: force the ring depth of 128-row tiles (0 = by tile size)
-#endif
-#ifndef KH_GEMM_WR
-#define KH_GEMM_WR 1  // waves along the rows of 64- and 128-row tiles (2: two waves per SIMD)
-#endif
-// Waves per workgroup along the tile's rows: with 2, eight waves split a
-// tile into 2 row halves x 4 column groups, two per SIMD, so one wave's
-// memory waits overlap the other's MFMAs (each weight is dequantised by both
-// row halves).
-constexpr int wr_for(int mt) { return KH_GEMM_WR == 2 && mt >= 4 ? 2 : 1; }
-constexpr int ring_depth(int bits, int mt) {
-  return KH_GEMM_P && mt == 8 ? KH_GEMM_P
-                              : (wr_for(mt) == 2 ? (bits == 8 ? 2 : 4) : (mt == 4 ? 2 : 4));
-}
+constexpr int kBandM = 4;     // m-tiles per band of the tile order (m fastest within a band)
+constexpr int kSplitCap = 256;  // split-K target: workgroups per launch (one per CU)
+// VALU ops scheduled after each MFMA when dequantising a step ahead
+constexpr int kInterleave = 2;
+constexpr int ring_depth(int bits, int mt) { return mt == 4 ? 2 : 4; }
 
 // Scale/bias chunk: the groups of P stages (P*128 codes) of every row of the
 // workgroup, copied to LDS by direct loads of SPIECE bytes.
@@ -196,7 +161,7 @@ struct ScaleChunk {
 // gtab[1 + tm] the expert of m-tile tm (w, scales and biases are [E, N, ..]
 // stacks); rowmap[m] is the output row of padded row m, or -1 for padding.
 template <int BITS, bool SF16, int MT, int GS, int NT, bool GR>
-__global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
+__global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     const u32x4* __restrict__ xh, const float* __restrict__ rscale,
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, float* __restrict__ part, void* __restrict__ out,
@@ -204,16 +169,14 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
     const int* __restrict__ gtab, const int* __restrict__ rowmap) {
   // NT 16-column MFMA tiles per wave: 4 (a 256-column tile) or 2 (half of
   // one, for the last partial round of a launch)
-  constexpr int WR = wr_for(MT);            // row halves
-  constexpr int KW = kWaves * WR;           // waves per workgroup
-  constexpr int MW = MT / WR;               // 16-row m-tiles per wave
+  constexpr int KW = kWaves;               // waves per workgroup
+  constexpr int MW = MT;                   // 16-row m-tiles per wave
   constexpr int BN = kWaves * NT * 16;
   constexpr int SUB = kBN / BN;           // workgroups per 256-column tile
   constexpr int BM = 16 * MT;
   constexpr int LW = BITS / 4;             // 16-byte code loads per lane per 16-row tile
   constexpr int SLOTS = 16 * BM;           // u32x4 activation slots per stage
   constexpr int DOPS = (SLOTS + 64 * KW - 1) / (64 * KW);  // activation loads per lane
-  static_assert(WR == 1 || SLOTS % (64 * KW) == 0, "every wave issues the same loads");
   constexpr int P = ring_depth(BITS, MT);  // stages in flight
   using SC = ScaleChunk<GS, P, BN, KW>;
   constexpr int LGS = __builtin_ctz(GS);
@@ -223,8 +186,7 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wc = WR == 1 ? wave : wave % kWaves;  // column group
-  const int wr = WR == 1 ? 0 : wave / kWaves;     // row half
+  const int wc = wave;  // column group
   const int col = lane & 15, lg = lane >> 4;
 
   // XCD-aware tile order: workgroup b runs on XCD b % 8; the work items of
@@ -242,11 +204,11 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
   const int sp = t / (cnt * SUB);
   const int tile = tile0 + u0 / SUB;
   int tn = tile % tiles_n, tm = tile / tiles_n;
-  if (KH_GEMM_GM > 1) {
-    // bands of GM m-tiles, m fastest within a band: the workgroups resident
+  {
+    // bands of kBandM m-tiles, m fastest within a band: the workgroups resident
     // on one XCD at a time share both activation panels and code rows in L2
-    const int b0 = (tile / (KH_GEMM_GM * tiles_n)) * KH_GEMM_GM;
-    const int bh = min(KH_GEMM_GM, tiles_m - b0);
+    const int b0 = (tile / (kBandM * tiles_n)) * kBandM;
+    const int bh = min(kBandM, tiles_m - b0);
     const int rr = tile - b0 * tiles_n;
     tm = b0 + rr % bh;
     tn = rr / bh;
@@ -286,7 +248,7 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
       for (int h = 0; h < LW; ++h) {
         const int code = kc + (BITS == 4 ? lg * 32 : h * 64 + lg * 16);
         const u32x4* src = reinterpret_cast<const u32x4*>(row + code * BITS / 32);
-        q[u][h] = KH_GEMM_NT ? __builtin_nontemporal_load(src) : *src;
+        q[u][h] = *src;
       }
     }
   };
@@ -382,13 +344,12 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
   // chunk when one of those was issued at p == 0 (1 <= p <= P - 2). The
   // prologue's stages go out in the plain order, which puts more ops after
   // their last activation load: the same counts only wait longer there.
-  constexpr bool SPREAD = KH_GEMM_SPREAD && (MT == 8 || (KH_GEMM_SPREAD4 && MT == 4)) &&
-                          (NT == 4 || (KH_GEMM_SPREAD2 && NT == 2)) && WR == 1 && DOPS % 4 == 0;
+  constexpr bool SPREAD = (MT == 8 || MT == 4) && DOPS % 4 == 0;
   // (code tile j goes out in part j: with NT = 2 parts 2 and 3 carry none)
   constexpr int WS0 = (NT == 4 ? LW : 0) + (P - 2) * (DOPS + OPS);
   // dequantisation a step ahead (measured 2-6% on the 4-bit gs64 prefill
   // shapes; group size 32 would spill with it)
-  constexpr int IL = GS >= 64 && WR == 1 ? KH_GEMM_IL : 0;
+  constexpr int IL = GS >= 64 ? kInterleave : 0;
   static_assert(WS0 + SC::OPS < 64, "vmcnt holds 6 bits");
   load_scales(0);
   __builtin_amdgcn_sched_barrier(0);
@@ -455,7 +416,7 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
         auto read_a = [&](u32x4 (&a)[MW], int j) {
 #pragma unroll
           for (int i = 0; i < MW; ++i) {
-            const int m = (wr * MW + i) * 16 + col, kb = step_off<BITS>(j, lg) >> 3;
+            const int m = i * 16 + col, kb = step_off<BITS>(j, lg) >> 3;
             a[i] = lds_b128_nowait(&As[p][m * 16 + (kb ^ (m & 15))]);
           }
         };
@@ -488,7 +449,7 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
           }
         };
         // IL: the operands of step j+1 are dequantised while the MFMAs of
-        // step j run, interleaved by the scheduler (KH_GEMM_IL VALU ops per MFMA)
+        // step j run, interleaved by the scheduler (kInterleave VALU ops per MFMA)
         u32x4 bq[2][NT];
         if constexpr (IL > 0) dequant(bq[0], 0);
 #pragma unroll
@@ -542,7 +503,7 @@ __global__ __launch_bounds__(64 * kWaves * wr_for(MT)) void gemm_kernel(
     __syncthreads();
 #pragma unroll
     for (int il = 0; il < MW; ++il) {
-      const int i = wr * MW + il;            // m-tile within the workgroup tile
+      const int i = il;  // m-tile within the workgroup tile
       if (i < i0 || i >= i0 + EP) continue;  // another pass (uniform per wave)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -616,7 +577,7 @@ GemmPlan plan_gemm(int M, int N, int K, int bits) {
   const int stages = K / kStage;
   const int tm = mt < kMaxMT ? 1 : p.tiles_m;
   int s = 1;
-  while (p.tiles_n * tm * s * 2 <= KH_GEMM_CAP && stages / (2 * s) >= 4) s *= 2;
+  while (p.tiles_n * tm * s * 2 <= kSplitCap && stages / (2 * s) >= 4) s *= 2;
   p.nsplit = s;
   p.kslice = ((stages + s - 1) / s) * kStage;
   p.nsplit = (K + p.kslice - 1) / p.kslice;
@@ -626,7 +587,7 @@ GemmPlan plan_gemm(int M, int N, int K, int bits) {
   // output element still accumulates over K in the same order: the rows are
   // bit-identical to the full-width kernel's.
   const int T = p.tiles_n * p.tiles_m, r = T % kCUs;
-  p.tail = (KH_GEMM_TAIL && mt == kMaxMT && p.nsplit == 1 && T > kCUs && r > 0 && r <= kCUs / 2) ? r : 0;
+  p.tail = (mt == kMaxMT && p.nsplit == 1 && T > kCUs && r > 0 && r <= kCUs / 2) ? r : 0;
   return p;
 }
 
@@ -642,7 +603,7 @@ static hipError_t launch_range(const QmvArgs& a, const GemmPlan& p, const u32x4*
                                const int* gtab, const int* rowmap) {
   const int total = cnt * (kNT / NT) * nsplit;
   const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
-  hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS, NT, GR>), dim3(grid), dim3(64 * kWaves * wr_for(MT)), 0,
+  hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS, NT, GR>), dim3(grid), dim3(64 * kWaves), 0,
                      a.stream, xh, rsc, (const uint32_t*)a.w, (const uint16_t*)a.scales,
                      (const uint16_t*)a.biases, part, a.out, a.odt, a.M, a.N, a.K, p.kslice,
                      p.tiles_n, tile0, cnt, nsplit, gtab, rowmap);

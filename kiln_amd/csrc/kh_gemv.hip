@@ -33,25 +33,11 @@
 
 namespace kh {
 
-#ifndef KH_GEMV_WAVES
-#define KH_GEMV_WAVES 2048  // waves per launch wanted before fewer rows per workgroup
-#endif
-#ifndef KH_GEMV_WAVES_WIDE
-#define KH_GEMV_WAVES_WIDE 4096  // ... and, while a workgroup keeps more than 4 rows, this many
-#endif
-
-#ifndef KH_GEMV_MAX_M
-#define KH_GEMV_MAX_M 8  // largest M served with one chunk per lane slot (4 or 8)
-#endif
-#ifndef KH_GEMV_RMAX
-#define KH_GEMV_RMAX 16  // rows per workgroup with one chunk per lane slot
-#endif
-#ifndef KH_GEMV_ABL
-#define KH_GEMV_ABL 0  // tuning ablations: 1 = no arithmetic on codes, 2 = no scale/bias loads
-#endif
-#ifndef KH_GEMV_NT
-#define KH_GEMV_NT 1  // weight loads marked non-temporal (streamed once)
-#endif
+// Plan constants (measured on the Llama-3 shapes):
+constexpr int kGemvWaves = 2048;      // waves per launch wanted before fewer rows per workgroup
+constexpr int kGemvWavesWide = 4096;  // ... and, while a workgroup keeps more than 4 rows, this many
+constexpr int kGemvMaxM1 = 8;         // largest M served with one chunk per lane slot
+constexpr int kGemvRMax = 16;         // rows per workgroup with one chunk per lane slot
 
 namespace {
 
@@ -66,7 +52,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7fffffff, 0x00020000);
 }
 
-constexpr int kCodeAux = KH_GEMV_NT ? 2 : 0;  // nt: weights are streamed once
+constexpr int kCodeAux = 2;  // non-temporal: weights are streamed once
 
 template <int BITS, bool XBF16>
 struct GemvOff {
@@ -292,13 +278,8 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
       q[r][i][2] = v[2];
       q[r][i][3] = v[3];
       const int go = (cidx[i] >> cshift) * 2;
-      if (KH_GEMV_ABL == 2) {
-        sr[r][i] = 0x3c00u + r;
-        br[r][i] = 0x3c00u + go;
-      } else {
-        sr[r][i] = __builtin_amdgcn_raw_buffer_load_b16(bs[h], go, n * G * 2, 0);
-        br[r][i] = __builtin_amdgcn_raw_buffer_load_b16(bb[h], go, n * G * 2, 0);
-      }
+      sr[r][i] = __builtin_amdgcn_raw_buffer_load_b16(bs[h], go, n * G * 2, 0);
+      br[r][i] = __builtin_amdgcn_raw_buffer_load_b16(bb[h], go, n * G * 2, 0);
     }
   }
 
@@ -338,10 +319,6 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int i = 0; i < I; ++i) {
-      if (KH_GEMV_ABL == 1) {
-        acc[r * M] += __uint_as_float((q[r][i][0] ^ q[r][i][1] ^ q[r][i][2] ^ q[r][i][3] ^ sr[r][i] ^ br[r][i]) & 0x3fffffffu);
-        continue;
-      }
       uint32_t p[NP];
       chunk_pairs<BITS, XBF16>(q[r][i], mag, p);
       const float sc = half_bits_to_f32<SBF16>(sr[r][i]);
@@ -392,12 +369,12 @@ GemvPlan plan_gemv(int N, int K, int bits) {
   int I = 1;
   while ((nch + 64 * I - 1) / (64 * I) > kGemvMaxWaves) ++I;
   const int waves = (nch + 64 * I - 1) / (64 * I);
-  int R = I == 1 ? KH_GEMV_RMAX : (I == 2 ? 4 : 2);
-  while (R > 2 && (int64_t)((N + R - 1) / R) * waves < KH_GEMV_WAVES) R >>= 1;
+  int R = I == 1 ? kGemvRMax : (I == 2 ? 4 : 2);
+  while (R > 2 && (int64_t)((N + R - 1) / R) * waves < kGemvWaves) R >>= 1;
   // measured: 4 rows per workgroup with twice the waves beats 8 on the
   // Llama-3-8B shapes (gate 8.84 -> 8.63 us), while 2 rows instead of 4
   // costs 11% on the Llama-3.2-1B layer at M = 4
-  while (R > 4 && (int64_t)((N + R - 1) / R) * waves < KH_GEMV_WAVES_WIDE) R >>= 1;
+  while (R > 4 && (int64_t)((N + R - 1) / R) * waves < kGemvWavesWide) R >>= 1;
   return {waves, I, R};
 }
 
@@ -524,7 +501,7 @@ bool gemv_fits(int64_t M, int64_t N, int64_t K, int bits, int gs) {
 
 int gemv_max_m(int K, int bits) {
   const int I = plan_gemv(1, K, bits).I;
-  return I == 1 ? KH_GEMV_MAX_M : (I == 2 ? 2 : (I <= 4 ? 1 : 0));
+  return I == 1 ? kGemvMaxM1 : (I == 2 ? 2 : (I <= 4 ? 1 : 0));
 }
 
 hipError_t launch_gemv(const QmvArgs& a) {

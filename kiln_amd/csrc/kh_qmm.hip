@@ -35,10 +35,7 @@ constexpr int KB = BK / 8;  // 8-element k-blocks per stage
 constexpr int WM = 128, WN = 64;  // wave tile
 constexpr int MT = WM / 16, NTL = WN / 16;
 constexpr int BPAD = 4;     // words of padding per k-block row of the code tile
-#ifndef KH_QMM_PF
-#define KH_QMM_PF 2
-#endif
-constexpr int PF = KH_QMM_PF;  // stages of global loads in flight
+constexpr int PF = 2;  // stages of global loads in flight
 
 // Pairs of codes as float16 (1024 + q) in both halves (exact for q < 1024).
 template <int BITS>

@@ -104,38 +104,11 @@ __device__ __forceinline__ float half_to_f32(uint32_t h) {
   return SBF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
 }
 
-#ifndef KH_QMV_NT
-#define KH_QMV_NT 0
-#endif
-// Weight-stream load (plain, or non-temporal when KH_QMV_NT is set).
-template <typename T>
-__device__ __forceinline__ T ldw(const T* p) {
-#if KH_QMV_NT
-  return __builtin_nontemporal_load(p);
-#else
-  return *p;
-#endif
-}
-
-#ifndef KH_QMV_ABL
-#define KH_QMV_ABL 0  // tuning ablations: 1 = no staging loads, 2 = no MFMA/epilogue, 3 = no X MFMA
-#endif
-#ifndef KH_QMV_INFLIGHT
-#define KH_QMV_INFLIGHT 16  // VGPRs per lane for one chunk of code loads
-#endif
-#ifndef KH_QMV_WAVE_TARGET
-#define KH_QMV_WAVE_TARGET 4096  // waves per launch to aim for
-#endif
-#ifndef KH_QMV_MAX_WAVES
-#define KH_QMV_MAX_WAVES 8  // waves per workgroup (row tiles x K slices)
-#endif
-#ifndef KH_QMV_MIN_WGS
-#define KH_QMV_MIN_WGS 256  // workgroups wanted before packing more row tiles per workgroup
-#endif
-#ifndef KH_QMV_LDS
-#define KH_QMV_LDS 49152  // LDS bytes per workgroup for staged operands
-#endif
-
+constexpr int kQmvInflight = 16;     // VGPRs per lane for one chunk of code loads
+constexpr int kQmvWaveTarget = 4096; // waves per launch to aim for
+constexpr int kQmvMaxWaves = 8;      // waves per workgroup (row tiles x K slices)
+constexpr int kQmvMinWgs = 256;      // workgroups wanted before packing more row tiles per workgroup
+constexpr int kQmvLds = 49152;       // LDS bytes per workgroup for staged operands
 
 constexpr int pow2_floor(int v) {
   int p = 1;
@@ -154,7 +127,7 @@ struct QmvGeom {
   static constexpr int NC = CB >= GS ? CB / GS : 1;   // groups (chains) per block
   static constexpr int BPG = GS > CB ? GS / CB : 1;   // blocks per group
   static constexpr int LGC = 4 / NC;            // lane groups per chain
-  static constexpr int U = KH_QMV_INFLIGHT / 8; // blocks per load chunk (two chunks in flight)
+  static constexpr int U = kQmvInflight / 8; // blocks per load chunk (two chunks in flight)
 };
 
 struct QmvPlan {
@@ -175,9 +148,9 @@ static QmvPlan plan_qmv_t(int M, int N, int K) {
   const int NU = ceil_div(K, Gm::CB) / Gm::BPG;  // units per row
   const int tiles16 = ceil_div(N, 16);
   int rt = 4;
-  while (rt > 1 && tiles16 / rt < KH_QMV_MIN_WGS) rt /= 2;
+  while (rt > 1 && tiles16 / rt < kQmvMinWgs) rt /= 2;
   int ks = 1;
-  while (rt * ks * 2 <= KH_QMV_MAX_WAVES && ceil_div(tiles16, rt) * rt * ks * 2 <= KH_QMV_WAVE_TARGET &&
+  while (rt * ks * 2 <= kQmvMaxWaves && ceil_div(tiles16, rt) * rt * ks * 2 <= kQmvWaveTarget &&
          NU / (ks * 2) >= 2)
     ks *= 2;
   const int rows = 16 * rt;
@@ -190,8 +163,8 @@ static QmvPlan plan_qmv_t(int M, int N, int K) {
   // LDS per staged unit: activations and raw scale/bias halves.
   const size_t per_unit = (size_t)Gm::BPG * Gm::CB * M * 2 + (size_t)rows * Gm::NC * 4;
   int batch = ks;
-  while (batch > 1 && per_unit * batch > KH_QMV_LDS) batch /= 2;
-  int wu = pow2_floor((int)(KH_QMV_LDS / (per_unit * batch)) > 0 ? (int)(KH_QMV_LDS / (per_unit * batch)) : 1);
+  while (batch > 1 && per_unit * batch > kQmvLds) batch /= 2;
+  int wu = pow2_floor((int)(kQmvLds / (per_unit * batch)) > 0 ? (int)(kQmvLds / (per_unit * batch)) : 1);
   while (wu > 1 && wu / 2 >= ceil_div(NU, ks)) wu /= 2;
   size_t lds = (size_t)batch * wu * per_unit + (size_t)Gm::SPB * M * 16;
   const size_t red = (size_t)rt * ks * 64 * 16 + (size_t)M * rows * 4;
@@ -200,7 +173,7 @@ static QmvPlan plan_qmv_t(int M, int N, int K) {
 }
 
 template <int BITS, int GS, bool XBF16, bool SBF16, int TILES>
-__global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
+__global__ __launch_bounds__(64 * kQmvMaxWaves) void qmv_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     void* __restrict__ out, int odt, int M, int N, int K, int RT, int nct, int wu, int batch) {
@@ -292,7 +265,7 @@ __global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
         // a lane chunk past the row end (partial last block) reads the row's
         // last chunk instead; its activations are zero
         const int word = min(blk * 16 + lg * 4, WR - 4);
-        const u32x4 v = ldw(reinterpret_cast<const u32x4*>(wrow + word));
+        const u32x4 v = *reinterpret_cast<const u32x4*>(wrow + word);
         q[u][0] = v[0];
         q[u][1] = v[1];
         q[u][2] = v[2];
@@ -315,7 +288,7 @@ __global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
         const int unit = ((NU * k_sl) >> lks) + off + ul;
         const int uend = (NU * (k_sl + 1)) >> lks;
         const int k = (unit * BPG * KBB + kb) * 8;
-        const bool ok = KH_QMV_ABL != 1 && unit < uend && k < K;
+        const bool ok = unit < uend && k < K;
         u32x4* dst = xs + (size_t)slot * xs_u + kb * M;
         for (int m = 0; m < M; ++m)
           dst[m] = ok ? permute_x<BITS>(*reinterpret_cast<const u32x4*>(x + (int64_t)m * K + k))
@@ -334,7 +307,7 @@ __global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
         const int g = unit * NC + c;
         const int rn = min(row0 + row, N - 1);
         uint32_t e = 0u;
-        if (KH_QMV_ABL != 1 && unit < uend && g < G)
+        if (unit < uend && g < G)
           e = (uint32_t)scales[(int64_t)rn * G + g] | ((uint32_t)biases[(int64_t)rn * G + g] << 16);
         sbh[((size_t)((sb_i << lwu) + ul) * ROWS + row) * NC + c] = e;
       }
@@ -354,10 +327,6 @@ __global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
         u32x4 B[SPB];
 #pragma unroll
         for (int j = 0; j < SPB; ++j) B[j] = codes_to_b<BITS, XBF16>(&q[u][j * WPS], mag);
-        if (KH_QMV_ABL == 2) {
-          acc[0][0] += __uint_as_float(B[0][0] ^ B[SPB - 1][3]);
-          continue;
-        }
         const int slot = slot0 + ul;
         const u32x4* xunit = xs + (size_t)slot * xs_u + bib * KBB * M;
         const uint32_t* sbu = sbh + ((size_t)slot * ROWS + rt * 16 + col) * NC;
@@ -369,7 +338,7 @@ __global__ __launch_bounds__(64 * KH_QMV_MAX_WAVES) void qmv_kernel(
           for (int j = 0; j < SPB; ++j) {
             const u32x4 a = ap[j * M];
             D[t] = mfma<XBF16>(a, B[j], D[t]);
-            if (KH_QMV_ABL != 3) DX[t] = mfma<XBF16>(a, ones, DX[t]);  // group sums X of the same rows
+            DX[t] = mfma<XBF16>(a, ones, DX[t]);  // group sums X of the same rows
           }
           if (bib == BPG - 1) {
             const uint32_t e = sbu[d_chain[t]];

@@ -191,24 +191,30 @@ int check_device(const char* op) {
   return it->second ? KH_OK : fail(KH_ERR_NO_DEVICE, "[%s] device %d is not gfx950", op, dev);
 }
 
-// Per (device, stream) workspace: a counter region (kept all-zero between
-// calls: the split-K decode kernel returns every counter it takes to zero)
-// followed by float scratch (split-K partials, prefill group sums). Grown on
-// demand — synchronising that stream first — and never shrunk, so the steady
-// state performs no allocation. Calls on one stream are ordered, so they can
-// share it.
-constexpr size_t kCounterBytes = 64 * 1024;
-
-// Buffers replaced while their stream was capturing: a graph may still refer
-// to them, so they live until the process ends.
+// Per (device, stream) workspace of float scratch (split-K partials, the
+// prefill GEMM's float16 activations and row scales, grouped-gather plans).
+// Grown on demand and never shrunk, so the steady state performs no
+// allocation; the first call that needs more than the stream's buffer holds
+// allocates (hipMalloc). Calls on one stream are ordered, so they can share it.
+//
+// A buffer that a HIP graph captured may be used by every later replay of
+// that graph, so once a slot has been handed out while its stream was
+// capturing, the buffer is never freed: when it has to grow it is retired
+// (kept until the process ends) and a new one is allocated. Buffers never
+// seen by a capture are freed after synchronising their stream.
 std::vector<void*>& retired() {
   static std::vector<void*> v;
   return v;
 }
 
 struct Workspace {
-  unsigned* counters;
   float* data;
+};
+
+struct WsSlot {
+  void* p = nullptr;
+  size_t bytes = 0;
+  bool captured = false;  // handed out to a capturing stream at least once
 };
 
 // `which` selects one of several independent buffers of the stream (0: the
@@ -217,47 +223,48 @@ struct Workspace {
 bool workspace(hipStream_t stream, size_t floats, Workspace* ws, int* rc, const char* op,
                int which = 0) {
   static std::mutex mu;
-  static std::map<std::tuple<int, hipStream_t, int>, std::pair<void*, size_t>> pool;
+  static std::map<std::tuple<int, hipStream_t, int>, WsSlot> pool;
   int dev = 0;
   (void)hipGetDevice(&dev);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(stream, &cs);
+  if (e != hipSuccess) {
+    *rc = hip_fail(op, e);
+    return false;
+  }
+  const bool capturing = cs != hipStreamCaptureStatusNone;
   std::lock_guard<std::mutex> lock(mu);
-  auto& slot = pool[{dev, stream, which}];
-  const size_t bytes = kCounterBytes + floats * sizeof(float);
-  if (slot.second < bytes) {
-    // Under stream capture (e.g. a HIP graph being recorded) the stream may
-    // not be synchronised and memory it may still use must not be freed: the
-    // old buffer is retired instead, the allocation runs in relaxed capture
-    // mode, and the counter-zeroing kernel becomes part of the graph.
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    hipError_t e = hipStreamIsCapturing(stream, &cs);
-    const bool capturing = e == hipSuccess && cs != hipStreamCaptureStatusNone;
-    if (e == hipSuccess && slot.first) {
-      if (capturing) {
-        retired().push_back(slot.first);
+  WsSlot& slot = pool[{dev, stream, which}];
+  const size_t bytes = floats * sizeof(float);
+  if (slot.bytes < bytes) {
+    if (slot.p) {
+      if (capturing || slot.captured) {
+        retired().push_back(slot.p);
       } else {
         e = hipStreamSynchronize(stream);
-        if (e == hipSuccess) e = hipFree(slot.first);
+        if (e == hipSuccess) e = hipFree(slot.p);
       }
     }
-    slot = {nullptr, 0};
+    slot = WsSlot{};
     void* p = nullptr;
     const size_t want = bytes < (size_t(4) << 20) ? (size_t(4) << 20) : bytes;
     if (e == hipSuccess) {
+      // under capture the allocation runs in relaxed capture mode
       hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
       if (capturing) (void)hipThreadExchangeStreamCaptureMode(&mode);
       e = hipMalloc(&p, want);
       if (capturing) (void)hipThreadExchangeStreamCaptureMode(&mode);
     }
-    if (e == hipSuccess) e = kh::launch_fill_u32(p, kCounterBytes / 4, 0u, stream);
     if (e != hipSuccess) {
       *rc = hip_fail(op, e);
       return false;
     }
-    slot = {p, want};
+    slot.p = p;
+    slot.bytes = want;
   }
+  slot.captured |= capturing;
   *rc = KH_OK;
-  ws->counters = static_cast<unsigned*>(slot.first);
-  ws->data = reinterpret_cast<float*>(static_cast<char*>(slot.first) + kCounterBytes);
+  ws->data = static_cast<float*>(slot.p);
   return true;
 }
 
@@ -318,26 +325,18 @@ bool fast_path(const kh::QmvArgs& a, bool transpose) {
          aligned16(a.w);
 }
 
-#ifndef KH_SKINNY_MIN_M
-#define KH_SKINNY_MIN_M 5  // smallest M the skinny MFMA kernel takes over from the GEMV (measured)
-#endif
-#ifndef KH_SKINNY_MIN_WAVES
-#define KH_SKINNY_MIN_WAVES 1024  // narrower skinny launches leave the GEMV the M it serves (measured)
-#endif
+constexpr int kSkinnyMinM = 5;         // smallest M the skinny MFMA kernel takes over from the GEMV (measured)
+constexpr int kSkinnyMinWaves = 1024;  // narrower skinny launches leave the GEMV the M it serves (measured)
 bool skinny_path(const kh::QmvArgs& a) {
-  if (a.M < KH_SKINNY_MIN_M || !kh::skinny_supported(a.M, a.N, a.K, a.bits, a.gs)) return false;
+  if (a.M < kSkinnyMinM || !kh::skinny_supported(a.M, a.N, a.K, a.bits, a.gs)) return false;
   // Narrow shapes (k/v 1024x4096: 64 workgroups, 512 waves) fill the chip
   // better through the decode GEMV up to its M limit (7.4 -> 6.3 us at
   // M = 8); a rule on N and K, so rows stay M-invariant within each kernel.
   return !(a.M <= kh::gemv_max_m(a.K, a.bits) && kh::gemv_fits(a.M, a.N, a.K, a.bits, a.gs) &&
-           kh::skinny_waves(a.N, a.K) < KH_SKINNY_MIN_WAVES);
+           kh::skinny_waves(a.N, a.K) < kSkinnyMinWaves);
 }
-#ifndef KH_GROUP_MIN_ROWS
-#define KH_GROUP_MIN_ROWS 64  // gather_qmm: fewest rows (pairs * M) for the grouped GEMM
-#endif
-#ifndef KH_GROUP_MIN_AVG
-#define KH_GROUP_MIN_AVG 2    // ... and fewest rows per possible expert group
-#endif
+constexpr int kGroupMinRows = 64;  // gather_qmm: fewest rows (pairs * M) for the grouped GEMM
+constexpr int kGroupMinAvg = 2;    // ... and fewest rows per possible expert group
 bool gemv_path(const kh::QmvArgs& a) {
   return a.M <= kh::gemv_max_m(a.K, a.bits) && kh::gemv_fits(a.M, a.N, a.K, a.bits, a.gs);
 }
@@ -400,6 +399,29 @@ int run_qmm(const char* op, const kh::QmvArgs& a, bool transpose) {
 }
 
 }  // namespace
+
+int kh_quantized_matmul_plan(int64_t M, int64_t N, int64_t K, int group_size, int bits, int x_dtype,
+                             int scales_dtype, char* buf, size_t len) {
+  if (!buf || len == 0) return fail(KH_ERR_INVALID_ARGUMENT, "[quantized_matmul_plan] buf is NULL");
+  if (M < 0 || N < 0 || K < 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[quantized_matmul_plan] M/N/K out of range");
+  alignas(16) static const char dummy[16] = {};
+  const kh::QmvArgs a{dummy, x_dtype, dummy, dummy, dummy, scales_dtype, nullptr, KH_FLOAT32,
+                      (int)M, (int)N, (int)K, group_size, bits, nullptr};
+  if (!fast_path(a, true)) {
+    snprintf(buf, len, "generic");
+  } else if (skinny_path(a)) {
+    snprintf(buf, len, "skinny");
+  } else if (gemv_path(a)) {
+    snprintf(buf, len, "gemv");
+  } else if (kh::gemm_supported((int)K)) {
+    const kh::GemmPlan p = kh::plan_gemm((int)M, (int)N, (int)K, bits);
+    snprintf(buf, len, "gemm mt=%d nsplit=%d tail=%d", p.mt, p.nsplit, p.tail);
+  } else {
+    snprintf(buf, len, M <= kh::kDecodeMaxM ? "qmv" : "qmm");
+  }
+  return KH_OK;
+}
 
 int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
                         const kh_array* scales, const kh_array* biases, bool transpose,
@@ -573,7 +595,7 @@ int kh_gather_qmm(kh_array* res, const kh_array* x, const kh_array* w, const kh_
   // GEMV does not take.
   const int64_t groups = std::min<int64_t>(E + 1, pairs), nrows = pairs * M;
   const bool grouped = fast && kh::gemm_supported((int)K) && E <= kh::kGroupMaxE &&
-                       (!gemv || (nrows >= KH_GROUP_MIN_ROWS && nrows >= KH_GROUP_MIN_AVG * groups));
+                       (!gemv || (nrows >= kGroupMinRows && nrows >= kGroupMinAvg * groups));
   if (grouped) {
     const kh::GroupPlan gp = kh::plan_group(a, g);
     if (gp.padded > INT32_MAX)

@@ -249,3 +249,14 @@ def quantized_embedding(ids: torch.Tensor, w: torch.Tensor, scales: torch.Tensor
         _desc(biases, "biases"), _lib.opt(group_size), _lib.opt(bits),
         mode.encode() if mode is not None else None, _stream_handle(w, stream)))
     return out
+
+
+def quantized_matmul_plan(M: int, N: int, K: int, group_size: int = 64, bits: int = 4,
+                          x_dtype: torch.dtype = torch.bfloat16,
+                          scales_dtype: torch.dtype = torch.float16) -> str:
+    """Name of the kernel plan quantized_matmul runs for a transpose=true call
+    of this shape (diagnostics; needs no GPU)."""
+    buf = ctypes.create_string_buffer(96)
+    _check(_lib.lib().kh_quantized_matmul_plan(M, N, K, group_size, bits, _TORCH_TO_KH[x_dtype],
+                                                _TORCH_TO_KH[scales_dtype], buf, len(buf)))
+    return buf.value.decode()

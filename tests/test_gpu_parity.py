@@ -303,6 +303,35 @@ def test_graph_capture_replays_match_eager(M, N, K):
         torch.cuda.synchronize()
 
 
+def test_graph_workspace_survives_eager_growth():
+    """A graph captured on a stream keeps using that stream's workspace; an
+    eager call afterwards on the same stream that needs a larger workspace
+    must not free the buffer the graph refers to. Every replay after the
+    growth still equals the eager result."""
+    print("case graph workspace growth", flush=True)
+    N, K = 1024, 2048
+    L, x = _case(40, N, K, 64, 4, seed=17)  # M = 40: the GEMM path (workspace user)
+    xd, w, s, b = dev(x, "bf16"), dev(L["w"]), dev(L["scales"], "f16"), dev(L["biases"], "f16")
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        eager = ops.quantized_matmul(xd, w, s, b, True, 64, 4, out_dtype="f32").clone()
+        out = torch.empty_like(eager)
+    st.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        ops.quantized_matmul(xd, w, s, b, True, 64, 4, out=out)
+    Lb, xb = _case(2048, N, K, 64, 4, seed=18)  # needs a workspace several times larger
+    big = [dev(xb, "bf16"), dev(Lb["w"]), dev(Lb["scales"], "f16"), dev(Lb["biases"], "f16")]
+    for r in range(3):
+        with torch.cuda.stream(st):
+            ops.quantized_matmul(*big, True, 64, 4, out_dtype="f32")
+            big[0] = torch.cat([big[0], big[0]])  # the next eager call grows it again
+            out.fill_(float("nan"))
+            g.replay()
+        st.synchronize()
+        assert torch.equal(out, eager), r
+
+
 @pytest.mark.parametrize("bits,gs,K", [(4, 32, 224), (4, 64, 192), (8, 32, 96), (8, 64, 320), (4, 32, 32)])
 @pytest.mark.parametrize("M", [1, 5, 16, 40])
 def test_qmm_partial_blocks(oracle, bits, gs, K, M):
