@@ -215,6 +215,26 @@ int kh_quantized_embedding(kh_array* res, const kh_array* ids,
  * res has a's shape. Each sum is formed in float32 and rounded once to res. */
 int kh_add(kh_array* res, const kh_array* a, const kh_array* b, kh_stream stream);
 
+/* kh_quantized_matmul without any device allocation. No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, validation and results (bit for bit) as kh_quantized_matmul.
+ * The kernels' scratch (the prefill GEMM's float16 activations, row scales and
+ * split-K partials) lives in one static device array per GPU of
+ * kh_noalloc_scratch_bytes() bytes (64 MiB), held until the process ends; a
+ * call that needs more fails with KH_ERR_UNSUPPORTED before launching
+ * anything (e.g. M*K*2 + 4*M plus, with split-K, 4*nsplit*M*N bytes above
+ * 64 MiB). Every call on one GPU shares that array: calls that overlap on one
+ * GPU (concurrent streams, or threads) race and must be serialised by the
+ * caller. Nothing in the array needs clearing between calls. */
+int kh_quantized_matmul_noalloc(kh_array* res, const kh_array* x, const kh_array* w,
+                                const kh_array* scales, const kh_array* biases,
+                                bool transpose, kh_optional_int group_size,
+                                kh_optional_int bits, const char* mode, kh_stream stream);
+
+/* Bytes of kh_quantized_matmul_noalloc's per-GPU scratch array. */
+size_t kh_noalloc_scratch_bytes(void);
+
 /* Diagnostics, no counterpart in the reference: writes to buf the name of the
  * kernel plan kh_quantized_matmul runs for a transpose=true call of this
  * shape and these dtypes with 16-byte aligned operands ("gemv", "skinny",

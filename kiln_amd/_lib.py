@@ -24,7 +24,8 @@ STATUS = {0: "KH_OK", 1: "KH_ERR_INVALID_ARGUMENT", 2: "KH_ERR_UNSUPPORTED",
 EXPORTS = ("kh_quantized_matmul", "kh_quantized_matmul_multi", "kh_quantized_gate_up",
            "kh_gather_qmm", "kh_quantize",
            "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add", "kh_last_error",
-           "kh_version", "kh_quantized_matmul_plan")
+           "kh_version", "kh_quantized_matmul_plan", "kh_quantized_matmul_noalloc",
+           "kh_noalloc_scratch_bytes")
 
 
 class KhArray(ctypes.Structure):
@@ -77,6 +78,9 @@ def lib() -> ctypes.CDLL:
                   "kh_gather_qmm", "kh_quantize",
                   "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add"):
             getattr(L, f).restype = ctypes.c_int
+        L.kh_quantized_matmul_noalloc.argtypes = L.kh_quantized_matmul.argtypes
+        L.kh_quantized_matmul_noalloc.restype = ctypes.c_int
+        L.kh_noalloc_scratch_bytes.restype = ctypes.c_size_t
         L.kh_quantized_matmul_plan.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
                                                ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                ctypes.c_char_p, ctypes.c_size_t]

@@ -220,8 +220,29 @@ struct WsSlot {
 // `which` selects one of several independent buffers of the stream (0: the
 // kernels' own scratch; 1: intermediates of a composite call whose steps use
 // buffer 0).
+// A caller-fixed scratch buffer that replaces the stream workspace for the
+// duration of one call on this thread (kh_quantized_matmul_noalloc).
+struct FixedScratch {
+  void* p;
+  size_t bytes;
+};
+thread_local const FixedScratch* g_fixed_scratch = nullptr;
+
 bool workspace(hipStream_t stream, size_t floats, Workspace* ws, int* rc, const char* op,
                int which = 0) {
+  if (g_fixed_scratch) {
+    const size_t need = floats * sizeof(float);
+    if (need > g_fixed_scratch->bytes) {
+      *rc = fail(KH_ERR_UNSUPPORTED,
+                 "[%s] this call needs %zu bytes of scratch; the fixed scratch holds %zu "
+                 "(use kh_quantized_matmul, which allocates a workspace)",
+                 op, need, g_fixed_scratch->bytes);
+      return false;
+    }
+    *rc = KH_OK;
+    ws->data = static_cast<float*>(g_fixed_scratch->p);
+    return true;
+  }
   static std::mutex mu;
   static std::map<std::tuple<int, hipStream_t, int>, WsSlot> pool;
   int dev = 0;
@@ -436,6 +457,63 @@ int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
   if ((rc = check_device(op))) return rc;
   return run_qmm(op, a, transpose);
 }
+
+static __device__ __align__(256) unsigned char scratch[size_t(64) << 20];
+
+namespace {
+
+// Scratch of kh_quantized_matmul_noalloc (`scratch` above): one array per device, allocated by
+// the runtime when the code object is loaded and held until the process
+// ends. Host code never uses the name `scratch` as an address: it is a
+// host-side stand-in. The device address comes from hipGetSymbolAddress, once
+// per device (with that device current), and is kept in g_scratch_ptr.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_device(const char* op, void** out) {
+  static std::mutex mu;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(op, e);
+  if (dev < 0 || dev >= kMaxDevices) return fail(KH_ERR_UNSUPPORTED, "[%s] device %d beyond %d", op, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(op, e);
+    if (!p) return fail(KH_ERR_DEVICE, "[%s] no device address for the scratch array", op);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KH_OK;
+}
+static_assert(sizeof(scratch) == kNoAllocScratchBytes, "scratch size");
+
+}  // namespace
+
+int kh_quantized_matmul_noalloc(kh_array* res, const kh_array* x, const kh_array* w,
+                                const kh_array* scales, const kh_array* biases, bool transpose,
+                                kh_optional_int group_size, kh_optional_int bits_opt, const char* mode,
+                                kh_stream stream) {
+  const char* op = "quantized_matmul_noalloc";
+  kh::QmvArgs a;
+  bool empty = false;
+  int rc = prepare_qmm(op, res, x, w, scales, biases, transpose, group_size, bits_opt, mode, stream, &a,
+                       &empty);
+  if (rc || empty) return rc;
+  if ((rc = check_device(op))) return rc;
+  void* p = nullptr;
+  if ((rc = scratch_for_device(op, &p))) return rc;
+  const FixedScratch fixed{p, kNoAllocScratchBytes};
+  g_fixed_scratch = &fixed;
+  rc = run_qmm(op, a, transpose);
+  g_fixed_scratch = nullptr;
+  return rc;
+}
+
+size_t kh_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
 
 int kh_quantized_matmul_multi(int n, kh_array* const* res, const kh_array* x,
                               const kh_array* const* w, const kh_array* const* scales,
