@@ -55,6 +55,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--m", type=int, default=None, help="batch rows of --profile decode (default 1)")
     ap.add_argument("--profile", choices=["decode", "decode8", "prefill", "traffic", "moe"], default=None,
                     help="run one workload for a profiler and exit (no JSON line): the M=1 decode "
                          "step, the M=2048 Llama-3-8B layer, or a copy of known size followed by "
@@ -132,7 +133,7 @@ def main():
     layers = layer_copies(shapes, gs, "q4")
     copies = len(layers)
     if args.profile:
-        profile_run(args.profile, torch, ops, layers, shapes, layer_fns, dev, gs, bits)
+        profile_run(args.profile, torch, ops, layers, shapes, layer_fns, dev, gs, bits, args.m)
         return
     step, per = layer_fns(layers, shapes, 1, gs, bits)
     step_us = timed_steps_us(torch, step, copies, args.steps, args.warmup, stream)
@@ -225,10 +226,10 @@ def timed_steps_us(torch, step, copies, steps, warmup, stream):
     return 1e3 * e0.elapsed_time(e1) / steps
 
 
-def profile_run(kind, torch, ops, layers, shapes, layer_fns, dev, gs, bits):
+def profile_run(kind, torch, ops, layers, shapes, layer_fns, dev, gs, bits, m=None):
     """Workloads for rocprofv3 (kernel trace or counters), eager launches."""
     if kind == "decode":
-        step, _ = layer_fns(layers, shapes, 1, gs, bits)
+        step, _ = layer_fns(layers, shapes, m or 1, gs, bits)
         for r in range(4 * len(layers)):
             step(r % len(layers))
     elif kind == "decode8":

@@ -34,13 +34,13 @@
 // one XCD share both the activation panels and the code rows in its L2.
 #include "kh_common.h"
 #include "kh_kernels.h"
+#include "kh_lds.h"
 
 namespace kh {
 
 namespace {
 
 typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 h2;
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kStage = 128;   // codes per K stage
 constexpr int kWaves = 4;
@@ -50,39 +50,10 @@ constexpr int kXcds = 8;
 constexpr int kMaxMT = 8;     // largest m tile: 128 rows
 constexpr int kCUs = 256;     // MI355X compute units
 
-// s_waitcnt vmcnt(N) leaving expcnt and lgkmcnt unconstrained (gfx9
-// encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
-template <int N>
-__device__ __forceinline__ void waitcnt_vm() {
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-}
-
 __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
-
-// LDS reads issued by inline asm, which the compiler's wait insertion does
-// not see: it treats an LDS read as possibly aliasing the direct-to-LDS
-// loads in flight and would put a full wait before it, exposing the LDS
-// latency at every read. The data read here was completed by the stage's
-// vmcnt wait and barrier. lds_wait_all() waits for these reads; ready(v)
-// orders a use of v after that wait.
-__device__ __forceinline__ uint32_t lds_u16_nowait(const void* p) {
-  uint32_t v;
-  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
-  asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(a));
-  return v;
-}
-__device__ __forceinline__ u32x4 lds_b128_nowait(const void* p) {
-  u32x4 v;
-  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
-  return v;
-}
-__device__ __forceinline__ void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::); }
-__device__ __forceinline__ void ready(uint32_t& v) { asm volatile("" : "+v"(v)); }
-__device__ __forceinline__ void ready(u32x4& v) { asm volatile("" : "+v"(v)); }
 
 // Pairs of codes as float16 (1024 + q) in both halves (exact for q < 1024),
 // in the pair order of permute_x: 4-bit word -> (c0,c4)(c1,c5)(c2,c6)(c3,c7);
