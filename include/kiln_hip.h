@@ -177,6 +177,48 @@ int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gat
                          const kh_array* biases_up, kh_optional_int group_size,
                          kh_optional_int bits, const char* mode, kh_stream stream);
 
+/* The gated MLP's activation (Kiln's Activation, crates/kiln-models/src/
+ * nn.rs:259-294): silu(gate) for llama/qwen, gelu_approx(gate) for gemma. */
+typedef enum kh_activation { KH_ACT_SILU = 0, KH_ACT_GELU_APPROX = 1 } kh_activation;
+
+/* Linear::forward (crates/kiln-models/src/nn.rs:79-102) in one launch:
+ * res = quantized_matmul(x, w, scales, biases, transpose=true) [+ bias].
+ * bias: NULL, or a float [N] vector (Qwen2's q/k/v, mlp_bias models). The
+ * product is an array of MLX's result dtype for (x, scales) (equal dtypes:
+ * that dtype; otherwise float32) and the sum is formed in float32 from that
+ * rounded product and the bias, then rounded to res, whose dtype must be the
+ * dtype of product + bias: bit-identical to kh_quantized_matmul into an array
+ * of the product's dtype followed by kh_add. Without a bias this is
+ * kh_quantized_matmul with transpose=true. */
+int kh_linear(kh_array* res, const kh_array* x, const kh_array* w, const kh_array* scales,
+              const kh_array* biases, const kh_array* bias, kh_optional_int group_size,
+              kh_optional_int bits, const char* mode, kh_stream stream);
+
+/* n Linear::forward calls on one x (q/k/v, nn.rs:724-726), as
+ * kh_quantized_matmul_multi with each part's optional bias (bias may be NULL
+ * for no biases at all, or hold NULL entries); each part's result equals
+ * kh_linear's. One launch where the decode GEMV applies. */
+int kh_linear_multi(int n, kh_array* const* res, const kh_array* x, const kh_array* const* w,
+                    const kh_array* const* scales, const kh_array* const* biases,
+                    const kh_array* const* bias, kh_optional_int group_size, kh_optional_int bits,
+                    const char* mode, kh_stream stream);
+
+/* Mlp::forward's input to down_proj (crates/kiln-models/src/nn.rs:284-294):
+ * res = act(gate_proj(x)) * up_proj(x), the projections as kh_linear (with
+ * optional biases bias_gate / bias_up), act = silu or gelu_approx
+ * (gelu_approx as nn.rs:221-235: 0.5x(1 + tanh(sqrt(2/pi)(x + 0.044715x^3)))
+ * with every intermediate rounded to res's dtype as the reference's arrays
+ * are; x^3 formed as (x*x)*x in float32). gate and up have equal shapes;
+ * with biases res's dtype must be that of kh_linear's result. One launch
+ * where the decode GEMV applies; kh_quantized_gate_up is this call with
+ * silu and no biases. */
+int kh_mlp_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gate,
+                   const kh_array* scales_gate, const kh_array* biases_gate,
+                   const kh_array* bias_gate, const kh_array* w_up, const kh_array* scales_up,
+                   const kh_array* biases_up, const kh_array* bias_up, int activation,
+                   kh_optional_int group_size, kh_optional_int bits, const char* mode,
+                   kh_stream stream);
+
 /* Quantized gather-matmul over expert stacks (mlx_gather_qmm with null
  * lhs_indices, bound at crates/kiln-mlx/src/ops.rs:390-429; called by
  * SwitchLinear::forward, crates/kiln-models/src/moe.rs:124-176, for the MoE

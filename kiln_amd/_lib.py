@@ -25,7 +25,10 @@ EXPORTS = ("kh_quantized_matmul", "kh_quantized_matmul_multi", "kh_quantized_gat
            "kh_gather_qmm", "kh_quantize",
            "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add", "kh_last_error",
            "kh_version", "kh_quantized_matmul_plan", "kh_quantized_matmul_noalloc",
-           "kh_noalloc_scratch_bytes")
+           "kh_noalloc_scratch_bytes", "kh_linear", "kh_linear_multi", "kh_mlp_gate_up")
+
+# kh_activation
+ACT_SILU, ACT_GELU_APPROX = 0, 1
 
 
 class KhArray(ctypes.Structure):
@@ -66,6 +69,12 @@ def lib() -> ctypes.CDLL:
                                     ctypes.c_char_p, ctypes.c_bool, ctypes.c_void_p]
         L.kh_quantized_gate_up.argtypes = [P, P, P, P, P, P, P, P, KhOptionalInt, KhOptionalInt,
                                            ctypes.c_char_p, ctypes.c_void_p]
+        L.kh_linear.argtypes = [P, P, P, P, P, P, KhOptionalInt, KhOptionalInt, ctypes.c_char_p,
+                                ctypes.c_void_p]
+        L.kh_linear_multi.argtypes = [ctypes.c_int, PP, P, PP, PP, PP, PP, KhOptionalInt, KhOptionalInt,
+                                      ctypes.c_char_p, ctypes.c_void_p]
+        L.kh_mlp_gate_up.argtypes = [P, P, P, P, P, P, P, P, P, P, ctypes.c_int, KhOptionalInt,
+                                     KhOptionalInt, ctypes.c_char_p, ctypes.c_void_p]
         L.kh_dequantize.argtypes = [P, P, P, P, KhOptionalInt, KhOptionalInt, ctypes.c_char_p,
                                     ctypes.c_void_p]
         L.kh_quantize.argtypes = [P, P, P, P, KhOptionalInt, KhOptionalInt, ctypes.c_char_p,
@@ -75,6 +84,7 @@ def lib() -> ctypes.CDLL:
         L.kh_quantized_embedding.argtypes = [P, P, P, P, P, KhOptionalInt, KhOptionalInt,
                                              ctypes.c_char_p, ctypes.c_void_p]
         for f in ("kh_quantized_matmul", "kh_quantized_matmul_multi", "kh_quantized_gate_up",
+                  "kh_linear", "kh_linear_multi", "kh_mlp_gate_up",
                   "kh_gather_qmm", "kh_quantize",
                   "kh_dequantize", "kh_take", "kh_quantized_embedding", "kh_add"):
             getattr(L, f).restype = ctypes.c_int

@@ -74,6 +74,44 @@ __device__ __forceinline__ float silu_mul(float g, float u, int dt) {
   return a * u;
 }
 
+// gelu_approx(gate) * up of Kiln's gemma MLP (crates/kiln-models/src/nn.rs:
+// 221-235, 284-294), with every intermediate an array of dtype dt as in the
+// reference's op graph (scalars are weak: converted to dt first):
+//   cube = g^3; inner = g + 0.044715*cube; scaled = sqrt(2/pi)*inner;
+//   gate = 1 + tanh(scaled); act = (0.5*g)*gate; result act*up,
+// each op evaluated in float32 and rounded to dt. The cube is formed as
+// (g*g)*g in float32 (MLX's power(x, 3) differs at most in the last float32
+// bit). Returned in float32 for the caller's single rounding store.
+__device__ __forceinline__ float gelu_mul(float g, float u, int dt) {
+  g = round_to(g, dt);
+  u = round_to(u, dt);
+  const float c1 = round_to(0.044715f, dt), c2 = round_to(0.7978845608028654f, dt);
+  const float cube = round_to((g * g) * g, dt);
+  const float inner = round_to(g + round_to(c1 * cube, dt), dt);
+  const float scaled = round_to(c2 * inner, dt);
+  const float gate = round_to(1.f + round_to(tanhf(scaled), dt), dt);
+  const float act = round_to(round_to(0.5f * g, dt) * gate, dt);
+  return act * u;
+}
+
+// Activation of the gated MLP (Kiln's Activation enum, nn.rs:259-294).
+enum : int { ACT_SILU = 0, ACT_GELU_APPROX = 1 };
+__device__ __forceinline__ float act_mul(float g, float u, int dt, int act) {
+  return act == ACT_GELU_APPROX ? gelu_mul(g, u, dt) : silu_mul(g, u, dt);
+}
+
+// Epilogue of Linear::forward (crates/kiln-models/src/nn.rs:79-102): the
+// product is an array of dtype ydt, then `+ bias` (ops::add) forms the sum of
+// that rounded product and the bias in float32; the caller's store rounds the
+// sum to the result dtype. Without a bias the product passes unchanged.
+struct Epilogue {
+  const void* bias;  // [N] or nullptr
+  int bdt, ydt;
+  __device__ __forceinline__ float operator()(float v, int64_t n) const {
+    return bias ? round_to(v, ydt) + load_as_f32(bias, bdt, n) : v;
+  }
+};
+
 // Round a pair to dt and pack the two 16-bit results (lo = a).
 __device__ __forceinline__ uint32_t pack2(float a, float b, int dt) {
   uint32_t ha = dt == DT_BF16 ? f32_to_bf16_bits(a) : f32_to_f16_bits(a);

@@ -131,7 +131,7 @@ template <int BITS>
 __global__ void qmm_generic_kernel(const void* __restrict__ x, int xdt,
                                    const uint32_t* __restrict__ w, const void* __restrict__ scales,
                                    const void* __restrict__ biases, int sdt, void* __restrict__ out,
-                                   int odt, int M, int N, int K, int gs, int transpose) {
+                                   int odt, int M, int N, int K, int gs, int transpose, Epilogue epi) {
   constexpr int CPW = 32 / BITS;
   constexpr uint32_t MASK = (1u << BITS) - 1u;
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
@@ -157,7 +157,7 @@ __global__ void qmm_generic_kernel(const void* __restrict__ x, int xdt,
       acc = fmaf(load_as_f32(x, xdt, (int64_t)m * K + k), wv, acc);
     }
   }
-  store_from_f32(out, odt, (int64_t)m * N + n, acc);
+  store_from_f32(out, odt, (int64_t)m * N + n, epi(acc, n));
   }
 }
 
@@ -208,11 +208,11 @@ __global__ void gather_generic_kernel(const void* __restrict__ x, int xdt, const
   }
 }
 
-__global__ void silu_mul_kernel(const void* __restrict__ g, const void* __restrict__ u,
-                                void* __restrict__ res, int dt, int64_t n) {
+__global__ void act_mul_kernel(const void* __restrict__ g, const void* __restrict__ u,
+                               void* __restrict__ res, int dt, int64_t n, int act) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  store_from_f32(res, dt, i, silu_mul(load_as_f32(g, dt, i), load_as_f32(u, dt, i), dt));
+  store_from_f32(res, dt, i, act_mul(load_as_f32(g, dt, i), load_as_f32(u, dt, i), dt, act));
 }
 
 __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
@@ -383,18 +383,18 @@ hipError_t launch_qmm_generic(const QmvArgs& a, bool transpose) {
   const uint32_t* wp = static_cast<const uint32_t*>(a.w);
   if (a.bits == 4)
     hipLaunchKernelGGL(qmm_generic_kernel<4>, grid, block, 0, a.stream, a.x, a.xdt, wp, a.scales,
-                       a.biases, a.sdt, a.out, a.odt, a.M, a.N, a.K, a.gs, transpose ? 1 : 0);
+                       a.biases, a.sdt, a.out, a.odt, a.M, a.N, a.K, a.gs, transpose ? 1 : 0, a.epi());
   else
     hipLaunchKernelGGL(qmm_generic_kernel<8>, grid, block, 0, a.stream, a.x, a.xdt, wp, a.scales,
-                       a.biases, a.sdt, a.out, a.odt, a.M, a.N, a.K, a.gs, transpose ? 1 : 0);
+                       a.biases, a.sdt, a.out, a.odt, a.M, a.N, a.K, a.gs, transpose ? 1 : 0, a.epi());
   return hipGetLastError();
 }
 
-hipError_t launch_silu_mul(const void* g, const void* u, void* res, int dt, int64_t n,
-                           hipStream_t stream) {
+hipError_t launch_act_mul(const void* g, const void* u, void* res, int dt, int64_t n, int act,
+                          hipStream_t stream) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, g, u, res,
-                     dt, n);
+  hipLaunchKernelGGL(act_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, g, u, res,
+                     dt, n, act);
   return hipGetLastError();
 }
 

@@ -137,7 +137,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, float* __restrict__ part, void* __restrict__ out,
     int odt, int M, int N, int K, int kslice, int tiles_n, int tile0, int cnt, int nsplit,
-    const int* __restrict__ gtab, const int* __restrict__ rowmap) {
+    const int* __restrict__ gtab, const int* __restrict__ rowmap, Epilogue epi) {
   // NT 16-column MFMA tiles per wave: 4 (a 256-column tile) or 2 (half of
   // one, for the last partial round of a launch)
   constexpr int KW = kWaves;               // waves per workgroup
@@ -498,7 +498,11 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
         m = rowmap[m];  // output row (split-K is never used here)
         if (m < 0) continue;
       }
-      const f32x4 v = *reinterpret_cast<const f32x4*>(&T[tidx(r, c)]);
+      f32x4 v = *reinterpret_cast<const f32x4*>(&T[tidx(r, c)]);
+      if (nsplit == 1 && epi.bias) {  // uniform
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = epi(v[k], min(n + k, N - 1));
+      }
       if (nsplit > 1) {
         float* dst = part + ((int64_t)sp * M + m) * N + n;
         if (vec) {
@@ -523,12 +527,12 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
 
 // out[m, n] = sum over slices s (in order) of part[s, m, n].
 __global__ void gemm_reduce(const float* __restrict__ part, void* __restrict__ out, int odt,
-                            int64_t MN, int nsplit) {
+                            int64_t MN, int N, int nsplit, Epilogue epi) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= MN) return;
   float s = part[i];
   for (int k = 1; k < nsplit; ++k) s += part[(int64_t)k * MN + i];
-  store_from_f32(out, odt, i, s);
+  store_from_f32(out, odt, i, epi(s, i % N));
 }
 
 }  // namespace
@@ -577,7 +581,7 @@ static hipError_t launch_range(const QmvArgs& a, const GemmPlan& p, const u32x4*
   hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS, NT, GR>), dim3(grid), dim3(64 * kWaves), 0,
                      a.stream, xh, rsc, (const uint32_t*)a.w, (const uint16_t*)a.scales,
                      (const uint16_t*)a.biases, part, a.out, a.odt, a.M, a.N, a.K, p.kslice,
-                     p.tiles_n, tile0, cnt, nsplit, gtab, rowmap);
+                     p.tiles_n, tile0, cnt, nsplit, gtab, rowmap, GR ? Epilogue{nullptr, 0, 0} : a.epi());
   return hipGetLastError();
 }
 
@@ -633,7 +637,7 @@ hipError_t launch_gemm(const QmvArgs& a, const GemmPlan& p, const void* xh, cons
   if (e != hipSuccess || p.nsplit == 1) return e;
   const int64_t MN = (int64_t)a.M * a.N;
   hipLaunchKernelGGL(gemm_reduce, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, a.stream, part,
-                     a.out, a.odt, MN, p.nsplit);
+                     a.out, a.odt, MN, a.N, p.nsplit, a.epi());
   return hipGetLastError();
 }
 

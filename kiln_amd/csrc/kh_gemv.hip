@@ -147,9 +147,13 @@ struct GemvParts {
   const uint16_t* scales[kGemvMaxParts];
   const uint16_t* biases[kGemvMaxParts];
   void* out[kGemvMaxParts];
+  const void* bias[kGemvMaxParts];  // Linear::forward's bias per part, or nullptr
+  int bdt[kGemvMaxParts];
   int N[kGemvMaxParts];
   int wg0[kGemvMaxParts];
   int nparts;
+  int ydt;  // dtype the products are rounded to before a bias is added
+  int act;  // GU: the gated MLP's activation (ACT_SILU, ACT_GELU_APPROX)
 };
 
 // Gather mode (gather_qmm): workgroup b computes rows [rb*R, rb*R+R) of
@@ -168,7 +172,7 @@ struct GemvGather {
 };
 
 // RT rows per workgroup: R rows of one part, or (GU) R = RT/2 rows of the
-// gate and the same R rows of the up projection, stored as silu(gate)*up.
+// gate and the same R rows of the up projection, stored as act(gate)*up.
 template <int BITS, bool XBF16, bool SBF16, int M, int RT, int I, bool GU>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
     const uint16_t* __restrict__ x, const GemvParts parts, const GemvGather gth, int odt, int Mrows,
@@ -346,7 +350,8 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
     for (int v = 1; v < W; ++v) s += red[v][tid];
     const int r = tid / M, m = tid % M;
     const int n = row0 + r;
-    if (n < N && m < Mrows) store_from_f32(outp, odt, (int64_t)m * N + n, s);
+    const Epilogue epi{parts.bias[part], parts.bdt[part], parts.ydt};
+    if (n < N && m < Mrows) store_from_f32(outp, odt, (int64_t)m * N + n, epi(s, n));
   }
   if (GU && tid < NV / 2) {  // partial j = r*M + m: gate rows first, then up rows
     float g = red[0][tid], u = red[0][tid + NV / 2];
@@ -356,7 +361,9 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
     }
     const int r = tid / M, m = tid % M;
     const int n = row0 + r;
-    if (n < N && m < Mrows) store_from_f32(parts.out[0], odt, (int64_t)m * N + n, silu_mul(g, u, odt));
+    const Epilogue eg{parts.bias[0], parts.bdt[0], parts.ydt}, eu{parts.bias[1], parts.bdt[1], parts.ydt};
+    if (n < N && m < Mrows)
+      store_from_f32(parts.out[0], odt, (int64_t)m * N + n, act_mul(eg(g, n), eu(u, n), odt, parts.act));
   }
 }
 
@@ -489,7 +496,10 @@ void set_part(GemvParts& P, int i, const QmvArgs& a) {
   P.scales[i] = (const uint16_t*)a.scales;
   P.biases[i] = (const uint16_t*)a.biases;
   P.out[i] = a.out;
+  P.bias[i] = a.bias;
+  P.bdt[i] = a.bdt;
   P.N[i] = a.N;
+  P.ydt = a.ydt;
 }
 
 }  // namespace
@@ -521,10 +531,11 @@ hipError_t launch_gemv_multi(const QmvArgs* a, int n) {
   return launch(L);
 }
 
-hipError_t launch_gemv_gate_up(const QmvArgs& gate, const QmvArgs& up) {
+hipError_t launch_gemv_gate_up(const QmvArgs& gate, const QmvArgs& up, int act) {
   if (gate.M < 1 || gate.M > gemv_max_m(gate.K, gate.bits) || gate.N != up.N) return hipErrorInvalidValue;
   GemvLaunch L{&gate, {}, 0, true, {}, 0};
   L.parts.nparts = 2;
+  L.parts.act = act;
   set_part(L.parts, 0, gate);
   set_part(L.parts, 1, up);
   return launch(L);

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kh_common.h"
+
 namespace kh {
 
 // Quantized matmul, transpose=true: x [M, K], w [N, K*bits/32],
@@ -19,6 +21,11 @@ struct QmvArgs {
   int odt;
   int M, N, K, gs, bits;
   hipStream_t stream;
+  // Linear::forward's optional bias [N] (nullptr: none), its dtype, and the
+  // dtype the product is rounded to before the bias is added.
+  const void* bias = nullptr;
+  int bdt = 0, ydt = 0;
+  Epilogue epi() const { return Epilogue{bias, bdt, ydt}; }
 };
 
 // Small batches (M <= kSkinnyMaxM, K % 128 == 0): weights streamed once,
@@ -91,9 +98,9 @@ hipError_t launch_gemv_gather(const QmvArgs& a, const GatherArgs& g);
 // Any dtype/alignment/M: one thread per output, float32 fma chain.
 hipError_t launch_gather_generic(const QmvArgs& a, const GatherArgs& g);
 
-// gate.out = silu(x gate^T) * (x up^T) (silu_mul sequence), one launch;
-// gate.N == up.N.
-hipError_t launch_gemv_gate_up(const QmvArgs& gate, const QmvArgs& up);
+// gate.out = act(x gate^T [+ gate.bias]) * (x up^T [+ up.bias]) (act_mul
+// sequence, act = ACT_SILU or ACT_GELU_APPROX), one launch; gate.N == up.N.
+hipError_t launch_gemv_gate_up(const QmvArgs& gate, const QmvArgs& up, int act);
 
 // Decode path (M <= kDecodeMaxM; correct up to M = 64), MFMA on unscaled
 // codes with per-group fp32 scaling.
@@ -158,14 +165,14 @@ hipError_t launch_embedding(const void* ids, bool ids_signed, int64_t T, const v
                             const void* scales, const void* biases, int sdt, void* out, int odt,
                             int64_t V, int64_t H, int gs, int bits, hipStream_t stream);
 
-// res[i] = silu_mul(g[i], u[i]) in dtype dt (g, u, res all of dtype dt).
 // Affine quantization of rows x K values (dtype wdt) into packed codes
 // [rows, K*bits/32] and scales/biases [rows, K/gs] of dtype wdt.
 hipError_t launch_quantize(const void* w, int wdt, void* wq, void* scales, void* biases,
                            int64_t rows, int64_t K, int gs, int bits, hipStream_t stream);
 
-hipError_t launch_silu_mul(const void* g, const void* u, void* res, int dt, int64_t n,
-                           hipStream_t stream);
+// res[i] = act_mul(g[i], u[i], dt, act) (g, u, res all of dtype dt).
+hipError_t launch_act_mul(const void* g, const void* u, void* res, int dt, int64_t n, int act,
+                          hipStream_t stream);
 
 // res[i] = a[i] + b[i % nb] (float32 sum, rounded once to rdt).
 hipError_t launch_add(const void* a, int adt, const void* b, int bdt, void* res, int rdt, int64_t n,

@@ -248,7 +248,7 @@ __global__ __launch_bounds__(NT) void qmm_kernel(const u32x4* __restrict__ xh,
                                                  const uint16_t* __restrict__ biases,
                                                  const float* __restrict__ rscale,
                                                  void* __restrict__ out, int odt, int M, int N,
-                                                 int K) {
+                                                 int K, Epilogue epi) {
   constexpr int CPW = 32 / BITS;
   constexpr int WPS = 8 / CPW;                 // words per 8-k block
   constexpr int WPR = BK / CPW;                // words per row per stage
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(NT) void qmm_kernel(const u32x4* __restrict__ xh,
 #pragma unroll
       for (int u = 0; u < NTL; ++u) {
         const int n = n0 + wn * WN + u * 16 + col;
-        if (n < N) store_from_f32(out, odt, (int64_t)m * N + n, acc[t][u][i] * rsc);
+        if (n < N) store_from_f32(out, odt, (int64_t)m * N + n, epi(acc[t][u][i] * rsc, n));
       }
     }
   }
@@ -427,11 +427,11 @@ static hipError_t launch_sf(const QmvArgs& a, const u32x4* xh, const float* rsc)
   if (a.sdt == DT_F16)
     hipLaunchKernelGGL((qmm_kernel<BITS, GS, true>), grid, block, 0, a.stream, xh,
                        (const uint32_t*)a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases,
-                       rsc, a.out, a.odt, a.M, a.N, a.K);
+                       rsc, a.out, a.odt, a.M, a.N, a.K, a.epi());
   else
     hipLaunchKernelGGL((qmm_kernel<BITS, GS, false>), grid, block, 0, a.stream, xh,
                        (const uint32_t*)a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases,
-                       rsc, a.out, a.odt, a.M, a.N, a.K);
+                       rsc, a.out, a.odt, a.M, a.N, a.K, a.epi());
   return hipGetLastError();
 }
 

@@ -176,7 +176,7 @@ template <int BITS, int GS, bool XBF16, bool SBF16, int TILES>
 __global__ __launch_bounds__(64 * kQmvMaxWaves) void qmv_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    void* __restrict__ out, int odt, int M, int N, int K, int RT, int nct, int wu, int batch) {
+    void* __restrict__ out, int odt, int M, int N, int K, int RT, int nct, int wu, int batch, Epilogue epi) {
   using Gm = QmvGeom<BITS, GS>;
   constexpr int CB = Gm::CB, SPB = Gm::SPB, WPS = Gm::WPS, KBB = Gm::KBB;
   constexpr int NC = Gm::NC, BPG = Gm::BPG, LGC = Gm::LGC, U = Gm::U;
@@ -393,7 +393,7 @@ __global__ __launch_bounds__(64 * kQmvMaxWaves) void qmv_kernel(
   for (int i = tid; i < M * ROWS; i += nthreads) {
     const int m = i >> lrows, row = i & (ROWS - 1);
     const int nn = row0 + row;
-    if (nn < N) store_from_f32(out, odt, (int64_t)m * N + nn, outacc[i]);
+    if (nn < N) store_from_f32(out, odt, (int64_t)m * N + nn, epi(outacc[i], nn));
   }
 }
 
@@ -404,7 +404,7 @@ static hipError_t launch_tiles(const QmvArgs& a) {
 #define KH_QMV_LAUNCH(TV)                                                                      \
   hipLaunchKernelGGL((qmv_kernel<BITS, GS, XBF16, SBF16, TV>), grid, block, p.lds, a.stream,  \
                      (const uint16_t*)a.x, (const uint32_t*)a.w, (const uint16_t*)a.scales,   \
-                     (const uint16_t*)a.biases, a.out, a.odt, a.M, a.N, a.K, p.rt, p.nct, p.wu, p.batch)
+                     (const uint16_t*)a.biases, a.out, a.odt, a.M, a.N, a.K, p.rt, p.nct, p.wu, p.batch, a.epi())
   switch (p.tiles) {
     case 1: KH_QMV_LAUNCH(1); break;
     case 2: KH_QMV_LAUNCH(2); break;

@@ -56,7 +56,7 @@ template <int BITS, bool XBF16, bool SBF16, int GS, int NTW, int MT>
 __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    void* __restrict__ out, int odt, int M, int N, int K, int ppw) {
+    void* __restrict__ out, int odt, int M, int N, int K, int ppw, Epilogue epi) {
   constexpr int GP = kPiece / GS;               // groups per piece
   constexpr bool SPLIT = XBF16 && BITS == 8;    // 8-bit codes as two nibble operands
   constexpr uint32_t MAG = XBF16 ? 0x43004300u : 0x64006400u;   // OFF in both halves
@@ -231,7 +231,7 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
     const int base = ((mt * NTW + t) * 4 + e) * 64 + l, stride = MT * NTW * 256;
     float v = red[base];
     for (int ww = 1; ww < W; ++ww) v += red[base + ww * stride];
-    store_from_f32(out, odt, (int64_t)m * N + n, v);
+    store_from_f32(out, odt, (int64_t)m * N + n, epi(v, n));
   }
 }
 
@@ -274,7 +274,7 @@ hipError_t launch_t(const QmvArgs& a, const SkinnyPlan& p) {
   hipLaunchKernelGGL((skinny_kernel<BITS, XBF16, SBF16, GS, NTW, MT>), dim3(wgs), dim3(64 * p.W), lds,
                      a.stream, (const uint16_t*)a.x, (const uint32_t*)a.w,
                      (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.out, a.odt, a.M, a.N,
-                     a.K, p.ppw);
+                     a.K, p.ppw, a.epi());
   return hipGetLastError();
 }
 

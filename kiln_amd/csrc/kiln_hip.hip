@@ -515,28 +515,53 @@ int kh_quantized_matmul_noalloc(kh_array* res, const kh_array* x, const kh_array
 
 size_t kh_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
 
+namespace {
+
+int prepare_bias(const char* op, const char* name, const kh_array* bias, const kh_array* res,
+                 kh::QmvArgs* a);
+
+// n linears on one x (parts with optional biases): one GEMV launch, one
+// activation conversion for the prefill GEMMs, or the parts one by one.
+int multi(const char* op, int n, kh_array* const* res, const kh_array* x, const kh_array* const* w,
+          const kh_array* const* scales, const kh_array* const* biases, const kh_array* const* bias,
+          bool transpose, kh_optional_int group_size, kh_optional_int bits, const char* mode,
+          kh_stream stream);
+
+}  // namespace
+
 int kh_quantized_matmul_multi(int n, kh_array* const* res, const kh_array* x,
                               const kh_array* const* w, const kh_array* const* scales,
                               const kh_array* const* biases, bool transpose,
                               kh_optional_int group_size, kh_optional_int bits, const char* mode,
                               kh_stream stream) {
-  const char* op = "quantized_matmul_multi";
+  return multi("quantized_matmul_multi", n, res, x, w, scales, biases, nullptr, transpose, group_size, bits,
+               mode, stream);
+}
+
+namespace {
+
+int multi(const char* op, int n, kh_array* const* res, const kh_array* x, const kh_array* const* w,
+          const kh_array* const* scales, const kh_array* const* biases, const kh_array* const* bias,
+          bool transpose, kh_optional_int group_size, kh_optional_int bits, const char* mode,
+          kh_stream stream) {
   if (n < 1 || !res || !w || !scales || !biases)
     return fail(KH_ERR_INVALID_ARGUMENT, "[%s] n must be >= 1 with non-null part arrays (n=%d)", op, n);
   std::vector<kh::QmvArgs> a(n);
   bool any_empty = false;
   for (int i = 0; i < n; ++i) {
     bool empty = false;
-    const int rc = prepare_qmm(op, res[i], x, w[i], scales[i], biases[i], transpose, group_size, bits, mode,
-                               stream, &a[i], &empty);
+    int rc = prepare_qmm(op, res[i], x, w[i], scales[i], biases[i], transpose, group_size, bits, mode,
+                         stream, &a[i], &empty);
     if (rc) return rc;
+    if (!empty && bias && (rc = prepare_bias(op, "bias", bias[i], res[i], &a[i]))) return rc;
     any_empty |= empty;
   }
   if (int rc = check_device(op)) return rc;
   if (any_empty) {  // some part has N == 0 (or M == 0): run the others one by one
     for (int i = 0; i < n; ++i) {
-      int rc = kh_quantized_matmul(res[i], x, w[i], scales[i], biases[i], transpose, group_size, bits,
-                                   mode, stream);
+      int rc = bias ? kh_linear(res[i], x, w[i], scales[i], biases[i], bias[i], group_size, bits, mode, stream)
+                    : kh_quantized_matmul(res[i], x, w[i], scales[i], biases[i], transpose, group_size, bits,
+                                          mode, stream);
       if (rc) return rc;
     }
     return KH_OK;
@@ -559,12 +584,50 @@ int kh_quantized_matmul_multi(int n, kh_array* const* res, const kh_array* x,
   return KH_OK;
 }
 
-int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gate,
-                         const kh_array* scales_gate, const kh_array* biases_gate,
-                         const kh_array* w_up, const kh_array* scales_up, const kh_array* biases_up,
-                         kh_optional_int group_size, kh_optional_int bits, const char* mode,
-                         kh_stream stream) {
-  const char* op = "quantized_gate_up";
+}  // namespace
+
+namespace {
+
+// MLX's result dtype of an op on two float arrays: equal dtypes keep theirs,
+// any other pair (float16 with bfloat16, or with float32) gives float32.
+int promote(int a, int b) { return a == b ? a : KH_FLOAT32; }
+
+// Linear::forward's optional bias (crates/kiln-models/src/nn.rs:98-100) for
+// a validated call *a: a float [N] vector; the product is an array of MLX's
+// result dtype for (x, scales) and res has the dtype of product + bias.
+int prepare_bias(const char* op, const char* name, const kh_array* bias, const kh_array* res,
+                 kh::QmvArgs* a) {
+  if (!bias) return KH_OK;
+  int rc;
+  if ((rc = check_array(bias, op, name))) return rc;
+  if (!is_float(bias->dtype))
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] %s must be float16/bfloat16/float32, got %s", op, name,
+                dtype_name(bias->dtype));
+  if (bias->ndim != 1 || bias->shape[0] != a->N)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] %s has shape %s, expected (%d)", op, name,
+                shape_str(bias).c_str(), a->N);
+  const int ydt = promote(a->xdt, a->sdt);
+  const int want = promote(ydt, bias->dtype);
+  if (res->dtype != want)
+    return fail(KH_ERR_INVALID_ARGUMENT,
+                "[%s] res is %s but the product (%s) plus %s (%s) is %s", op, dtype_name(res->dtype),
+                dtype_name(ydt), name, dtype_name(bias->dtype), dtype_name(want));
+  a->bias = bias->data;
+  a->bdt = bias->dtype;
+  a->ydt = ydt;
+  return KH_OK;
+}
+
+// The gated MLP's input to its down projection: act(gate(x)) * up(x), the
+// linears with optional biases.
+int gate_up(const char* op, kh_array* res, const kh_array* x, const kh_array* w_gate,
+            const kh_array* scales_gate, const kh_array* biases_gate, const kh_array* bias_gate,
+            const kh_array* w_up, const kh_array* scales_up, const kh_array* biases_up,
+            const kh_array* bias_up, int activation, kh_optional_int group_size, kh_optional_int bits,
+            const char* mode, kh_stream stream) {
+  if (activation != KH_ACT_SILU && activation != KH_ACT_GELU_APPROX)
+    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] activation %d (supported: silu 0, gelu_approx 1)", op,
+                activation);
   kh::QmvArgs g, u;
   bool eg = false, eu = false;
   int rc = prepare_qmm(op, res, x, w_gate, scales_gate, biases_gate, true, group_size, bits, mode, stream,
@@ -574,9 +637,12 @@ int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gat
                         &eu)))
     return rc;
   if (eg || eu) return KH_OK;
+  if ((rc = prepare_bias(op, "bias_gate", bias_gate, res, &g)) ||
+      (rc = prepare_bias(op, "bias_up", bias_up, res, &u)))
+    return rc;
   if ((rc = check_device(op))) return rc;
   if (fast_path(g, true) && fast_path(u, true) && gemv_path(g) && !skinny_path(g) && g.sdt == u.sdt) {
-    const hipError_t e = kh::launch_gemv_gate_up(g, u);
+    const hipError_t e = kh::launch_gemv_gate_up(g, u, activation);
     return e == hipSuccess ? KH_OK : hip_fail(op, e);
   }
   // Composite: gate and up into intermediates of the result dtype (workspace
@@ -595,8 +661,49 @@ int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gat
     if ((rc = run_qmm(op, g, true))) return rc;
     if ((rc = run_qmm(op, u, true))) return rc;
   }
-  const hipError_t e = kh::launch_silu_mul(gbuf, ubuf, res->data, res->dtype, (int64_t)count, g.stream);
+  const hipError_t e =
+      kh::launch_act_mul(gbuf, ubuf, res->data, res->dtype, (int64_t)count, activation, g.stream);
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
+}
+
+}  // namespace
+
+int kh_quantized_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gate,
+                         const kh_array* scales_gate, const kh_array* biases_gate,
+                         const kh_array* w_up, const kh_array* scales_up, const kh_array* biases_up,
+                         kh_optional_int group_size, kh_optional_int bits, const char* mode,
+                         kh_stream stream) {
+  return gate_up("quantized_gate_up", res, x, w_gate, scales_gate, biases_gate, nullptr, w_up, scales_up,
+                 biases_up, nullptr, KH_ACT_SILU, group_size, bits, mode, stream);
+}
+
+int kh_mlp_gate_up(kh_array* res, const kh_array* x, const kh_array* w_gate, const kh_array* scales_gate,
+                   const kh_array* biases_gate, const kh_array* bias_gate, const kh_array* w_up,
+                   const kh_array* scales_up, const kh_array* biases_up, const kh_array* bias_up,
+                   int activation, kh_optional_int group_size, kh_optional_int bits, const char* mode,
+                   kh_stream stream) {
+  return gate_up("mlp_gate_up", res, x, w_gate, scales_gate, biases_gate, bias_gate, w_up, scales_up,
+                 biases_up, bias_up, activation, group_size, bits, mode, stream);
+}
+
+int kh_linear(kh_array* res, const kh_array* x, const kh_array* w, const kh_array* scales,
+              const kh_array* biases, const kh_array* bias, kh_optional_int group_size,
+              kh_optional_int bits, const char* mode, kh_stream stream) {
+  const char* op = "linear";
+  kh::QmvArgs a;
+  bool empty = false;
+  int rc = prepare_qmm(op, res, x, w, scales, biases, true, group_size, bits, mode, stream, &a, &empty);
+  if (rc || empty) return rc;
+  if ((rc = prepare_bias(op, "bias", bias, res, &a))) return rc;
+  if ((rc = check_device(op))) return rc;
+  return run_qmm(op, a, true);
+}
+
+int kh_linear_multi(int n, kh_array* const* res, const kh_array* x, const kh_array* const* w,
+                    const kh_array* const* scales, const kh_array* const* biases,
+                    const kh_array* const* bias, kh_optional_int group_size, kh_optional_int bits,
+                    const char* mode, kh_stream stream) {
+  return multi("linear_multi", n, res, x, w, scales, biases, bias, true, group_size, bits, mode, stream);
 }
 
 int kh_gather_qmm(kh_array* res, const kh_array* x, const kh_array* w, const kh_array* scales,

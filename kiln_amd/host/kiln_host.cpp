@@ -393,6 +393,25 @@ Result<Array> add(const Array& a, const Array& b, const Stream& s) {
   return out;
 }
 
+Result<Array> linear(const Array& x, const Array& w, const Array& scales, const Array& biases,
+                     const std::optional<Array>& bias, int group_size, int bits, const Stream& s) {
+  if (x.ndim() < 1 || w.ndim() != 2) return Error{"[linear] x must be [..., K] and w 2-D"};
+  std::vector<int64_t> shape = x.shape();
+  shape.back() = w.dim(0);
+  Dtype dt = promote(x.dtype(), scales.dtype());
+  if (bias) dt = promote(dt, bias->dtype());
+  auto r = Array::empty(shape, dt, s);
+  if (!r) return r;
+  Array out = r.take();
+  kh_array res = out.desc(), xd = x.desc(), wd = w.desc(), sd = scales.desc(), bd = biases.desc();
+  kh_array bsd{};
+  if (bias) bsd = bias->desc();
+  const int st = kh_linear(&res, &xd, &wd, &sd, &bd, bias ? &bsd : nullptr, opt(group_size), opt(bits),
+                           "affine", s.raw());
+  if (st) return kh_error(st);
+  return out;
+}
+
 }  // namespace ops
 
 // ---------------------------------------------------------------------------
@@ -586,9 +605,48 @@ Result<Linear> Linear::load(WeightStore& store, const std::string& prefix,
 
 Result<Array> Linear::forward(const Array& x, const Stream& s) const {
   if (!quantized_) return Error{"dense Linear is outside the quantized path this library implements"};
-  auto y = ops::quantized_matmul(x, weight_, scales_, biases_, true, group_size_, bits_, s);
-  if (!y || !bias_) return y;
-  return ops::add(y.value(), *bias_, s);
+  return ops::linear(x, weight_, scales_, biases_, bias_, group_size_, bits_, s);
+}
+
+Result<Mlp> Mlp::load(WeightStore& store, const std::string& prefix, const std::optional<Quantization>& q,
+                      Activation activation) {
+  Mlp m;
+  auto g = Linear::load(store, prefix + ".gate_proj", q);
+  if (!g) return g.error();
+  auto u = Linear::load(store, prefix + ".up_proj", q);
+  if (!u) return u.error();
+  auto d = Linear::load(store, prefix + ".down_proj", q);
+  if (!d) return d.error();
+  m.gate_proj_ = g.take();
+  m.up_proj_ = u.take();
+  m.down_proj_ = d.take();
+  m.activation_ = activation;
+  return m;
+}
+
+Result<Array> Mlp::forward(const Array& x, const Stream& s) const {
+  const Linear& g = gate_proj_;
+  const Linear& u = up_proj_;
+  if (!g.quantized_ || !u.quantized_)
+    return Error{"dense Linear is outside the quantized path this library implements"};
+  std::vector<int64_t> shape = x.shape();
+  shape.back() = g.weight_.dim(0);
+  Dtype dt = ops::promote(x.dtype(), g.scales_.dtype());
+  if (g.bias_) dt = ops::promote(dt, g.bias_->dtype());
+  auto r = Array::empty(shape, dt, s);
+  if (!r) return r.error();
+  Array act = r.take();
+  kh_array res = act.desc(), xd = x.desc();
+  kh_array gw = g.weight_.desc(), gs = g.scales_.desc(), gb = g.biases_.desc();
+  kh_array uw = u.weight_.desc(), us = u.scales_.desc(), ub = u.biases_.desc();
+  kh_array gbias{}, ubias{};
+  if (g.bias_) gbias = g.bias_->desc();
+  if (u.bias_) ubias = u.bias_->desc();
+  const int st = kh_mlp_gate_up(&res, &xd, &gw, &gs, &gb, g.bias_ ? &gbias : nullptr, &uw, &us, &ub,
+                                u.bias_ ? &ubias : nullptr, static_cast<int>(activation_),
+                                ops::opt(g.group_size_), ops::opt(g.bits_), "affine", s.raw());
+  if (st) return kh_error(st);
+  return down_proj_.forward(act, s);
 }
 
 std::pair<int64_t, int64_t> Linear::io_features() const {

@@ -177,6 +177,10 @@ Result<Array> quantized_embedding(const Array& ids, const Array& w, const Array&
 // a + b with b broadcast over a's leading dims (b.shape == a.shape[-b.ndim:]);
 // the Linear bias add of nn.rs:98-100.
 Result<Array> add(const Array& a, const Array& b, const Stream& s);
+// Linear::forward's quantized matmul (transpose=true) and optional bias in
+// one launch (kh_linear): the product in its own dtype, then + bias.
+Result<Array> linear(const Array& x, const Array& w, const Array& scales, const Array& biases,
+                     const std::optional<Array>& bias, int group_size, int bits, const Stream& s);
 }  // namespace ops
 
 // safetensors checkpoint store: weights.rs:37-130 (single file or sharded
@@ -217,10 +221,27 @@ class Linear {
   bool quantized() const { return quantized_; }
 
  private:
+  friend class Mlp;
   bool quantized_ = false;
   Array weight_, scales_, biases_;
   std::optional<Array> bias_;
   int group_size_ = 64, bits_ = 4;
+};
+
+// The gated MLP's activation (nn.rs:259-294).
+enum class Activation { Silu = KH_ACT_SILU, GeluApprox = KH_ACT_GELU_APPROX };
+
+// Mlp (nn.rs:259-294): down(act(gate(x)) * up(x)), the gate/up half in one
+// kh_mlp_gate_up call (one launch at decode sizes).
+class Mlp {
+ public:
+  static Result<Mlp> load(WeightStore& store, const std::string& prefix,
+                          const std::optional<Quantization>& q, Activation activation);
+  Result<Array> forward(const Array& x, const Stream& s) const;
+
+ private:
+  Linear gate_proj_, up_proj_, down_proj_;
+  Activation activation_ = Activation::Silu;
 };
 
 // Embedding (nn.rs:116-194): quantized or dense, also the tied LM head.

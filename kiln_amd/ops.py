@@ -178,6 +178,63 @@ def quantized_gate_up(x: torch.Tensor, gate, up, group_size: int = 64, bits: int
     return out
 
 
+def _bias_out_dtype(x, sc, bias):
+    y = result_dtype(x.dtype, sc.dtype)
+    return y if bias is None else result_dtype(y, bias.dtype)
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+           bias: torch.Tensor | None = None, group_size: int = 64, bits: int = 4, *,
+           mode: str = "affine", out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Linear::forward (crates/kiln-models/src/nn.rs:79-102): the quantized
+    matmul (transpose=true) plus the optional bias, in one launch."""
+    if out is None:
+        out = torch.empty((*x.shape[:-1], w.shape[0]), dtype=_bias_out_dtype(x, scales, bias),
+                          device=x.device)
+    _check(_lib.lib().kh_linear(
+        _desc(out, "res"), _desc(x, "x"), _packed(w), _desc(scales, "scales"), _desc(biases, "biases"),
+        None if bias is None else ctypes.byref(_desc(bias, "bias")), _lib.opt(group_size),
+        _lib.opt(bits), mode.encode() if mode is not None else None, _stream_handle(x, stream)))
+    return out
+
+
+def linear_multi(x: torch.Tensor, parts, group_size: int = 64, bits: int = 4, *, mode: str = "affine",
+                 outs=None, stream=None):
+    """[Linear::forward(x) for (w, scales, biases, bias) in parts] (q/k/v)."""
+    if outs is None:
+        outs = [torch.empty((*x.shape[:-1], w.shape[0]), dtype=_bias_out_dtype(x, sc, bi), device=x.device)
+                for w, sc, _, bi in parts]
+    res, k0 = _ptrs([_desc(o, "res") for o in outs])
+    ws, k1 = _ptrs([_packed(w) for w, _, _, _ in parts])
+    ss, k2 = _ptrs([_desc(sc, "scales") for _, sc, _, _ in parts])
+    bs, k3 = _ptrs([_desc(b, "biases") for _, _, b, _ in parts])
+    descs = [None if bi is None else _desc(bi, "bias") for _, _, _, bi in parts]
+    P = ctypes.POINTER(_lib.KhArray)
+    barr = (P * len(parts))(*[P() if d is None else ctypes.pointer(d) for d in descs])
+    _check(_lib.lib().kh_linear_multi(
+        len(parts), res, _desc(x, "x"), ws, ss, bs, barr, _lib.opt(group_size), _lib.opt(bits),
+        mode.encode() if mode is not None else None, _stream_handle(x, stream)))
+    return outs
+
+
+def mlp_gate_up(x: torch.Tensor, gate, up, activation: int = _lib.ACT_SILU, group_size: int = 64,
+                bits: int = 4, *, mode: str = "affine", out: torch.Tensor | None = None,
+                stream=None) -> torch.Tensor:
+    """act(gate_proj(x)) * up_proj(x) of Mlp::forward (nn.rs:284-294); gate and
+    up are (w, scales, biases, bias-or-None); activation ACT_SILU or
+    ACT_GELU_APPROX."""
+    if out is None:
+        out = torch.empty((*x.shape[:-1], gate[0].shape[0]), dtype=_bias_out_dtype(x, gate[1], gate[3]),
+                          device=x.device)
+    opt_b = lambda t, n: None if t is None else ctypes.byref(_desc(t, n))
+    _check(_lib.lib().kh_mlp_gate_up(
+        _desc(out, "res"), _desc(x, "x"), _packed(gate[0]), _desc(gate[1], "scales_gate"),
+        _desc(gate[2], "biases_gate"), opt_b(gate[3], "bias_gate"), _packed(up[0]), _desc(up[1], "scales_up"),
+        _desc(up[2], "biases_up"), opt_b(up[3], "bias_up"), int(activation), _lib.opt(group_size),
+        _lib.opt(bits), mode.encode() if mode is not None else None, _stream_handle(x, stream)))
+    return out
+
+
 def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
                group_size: int = 64, bits: int = 4, *, mode: str = "affine", out_dtype=None,
                out: torch.Tensor | None = None, stream=None) -> torch.Tensor:

@@ -293,3 +293,36 @@ def silu_mul(g: np.ndarray, u: np.ndarray, dt: str) -> np.ndarray:
         sg = to_f32(from_f32(np.float32(1) / (np.float32(1) + np.exp(-gf)), dt), dt)
     a = to_f32(from_f32(gf * sg, dt), dt)
     return from_f32(a * uf, dt)
+
+
+def gelu_mul(g: np.ndarray, u: np.ndarray, dt: str) -> np.ndarray:
+    """gelu_approx(gate) * up as Kiln's gemma MLP forms it (crates/kiln-
+    models/src/nn.rs:221-235 and 284-294), each op's result an array of
+    dtype dt (weak scalars converted to dt first), every op evaluated in
+    float32: cube = (g*g)*g; inner = g + c1*cube; scaled = c2*inner;
+    gate = 1 + tanh(scaled); act = (0.5*g)*gate; result act*up. Returns
+    stored values of dt."""
+    f32 = np.float32
+    r = lambda v: to_f32(from_f32(np.asarray(v, dtype=f32), dt), dt)
+    gf, uf = to_f32(g, dt), to_f32(u, dt)
+    c1, c2 = r(f32(0.044715)), r(f32(np.sqrt(2.0 / np.pi)))
+    with np.errstate(over="ignore", invalid="ignore"):
+        cube = r((gf * gf) * gf)
+        inner = r(gf + r(c1 * cube))
+        scaled = r(c2 * inner)
+        gate = r(f32(1) + r(np.tanh(scaled)))
+        act = r(r(f32(0.5) * gf) * gate)
+    return from_f32(act * uf, dt)
+
+
+def linear(x, xdt, w, s, b, sdt, gs, bits, bias=None, bdt=None, odt=None):
+    """Linear::forward (nn.rs:79-102): the quantized matmul as an array of
+    MLX's result dtype for (x, scales), then + bias (the sum of the rounded
+    product and the bias formed in float32, rounded to the sum's dtype).
+    Returns (stored values, dtype)."""
+    ydt = result_dtype(xdt, sdt)
+    y = quantized_matmul(x, xdt, w, s, b, sdt, gs, bits, True, ydt)
+    if bias is None:
+        return y, ydt
+    rdt = odt or (ydt if ydt == bdt else "f32")
+    return from_f32(to_f32(y, ydt) + to_f32(bias, bdt)[None, :], rdt), rdt

@@ -5,7 +5,7 @@
 //   kiln_host_run job <job.json>      loads a checkpoint directory and runs one
 //                                     layer call on the GPU, writing raw output
 //
-// job.json: {"model_dir": d, "op": "linear"|"embed"|"as_linear"|"probe"|"load",
+// job.json: {"model_dir": d, "op": "linear"|"mlp"|"embed"|"as_linear"|"probe"|"load"|"switch",
 //            "prefix": p, "input": file, "input_shape": [...],
 //            "input_dtype": "bfloat16"|"float16"|"float32"|"uint32"|"int32",
 //            "output": file}
@@ -150,6 +150,12 @@ static int job(const std::string& path) {
                                      quant.value(), s);
     if (!sl) return fail_json(sl.error().message);
     y = sl.value().forward(x.value(), ids.value(), j.get("sorted") && j.get("sorted")->b, s);
+  } else if (op == "mlp") {  // Mlp: prefix = the MLP prefix; "activation": "silu" | "gelu_approx"
+    const auto* act = j.get("activation");
+    const nn::Activation a = act && act->str == "gelu_approx" ? nn::Activation::GeluApprox : nn::Activation::Silu;
+    auto m = nn::Mlp::load(store.value(), prefix, quant.value(), a);
+    if (!m) return fail_json(m.error().message);
+    y = m.value().forward(x.value(), s);
   } else if (op == "linear") {
     auto l = nn::Linear::load(store.value(), prefix, quant.value());
     if (!l) return fail_json(l.error().message);

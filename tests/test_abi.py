@@ -281,3 +281,58 @@ def test_quantize_without_gpu_reports_no_device():
     # empty inputs succeed without touching the device
     assert _quantize(A(_lib.UINT32, (0, 16)), A(_lib.FLOAT32, (0, 2)), A(_lib.FLOAT32, (0, 2)),
                      A(_lib.FLOAT32, (0, 128))) == 0
+
+
+def _linear(res, x, w, s, b, bias, gs=64, bits=4):
+    return _lib.lib().kh_linear(ctypes.byref(res), ctypes.byref(x), ctypes.byref(w), ctypes.byref(s),
+                                ctypes.byref(b), None if bias is None else ctypes.byref(bias),
+                                _lib.opt(gs), _lib.opt(bits), b"affine", None)
+
+
+def test_linear_bias_validation():
+    """kh_linear (Linear::forward, nn.rs:79-102): the bias is a float [N]
+    vector and res has the dtype of product + bias (MLX promotion)."""
+    res, x, w, s, b = good()          # bf16 x, f16 scales: the product is float32
+    res32 = A(_lib.FLOAT32, (1, 32))
+    assert _linear(res32, x, w, s, b, A(_lib.BFLOAT16, (31,))) == 1
+    assert "bias has shape (31)" in _lib.last_error()
+    assert _linear(res32, x, w, s, b, A(_lib.INT32, (32,))) == 1
+    assert "bias must be" in _lib.last_error()
+    assert _linear(res, x, w, s, b, A(_lib.BFLOAT16, (32,))) == 1   # res must be float32 here
+    assert "float32" in _lib.last_error()
+    xs = A(_lib.FLOAT16, (1, 128))                                    # f16 x, f16 scales: f16 product
+    assert _linear(A(_lib.FLOAT16, (1, 32)), xs, w, s, b, A(_lib.FLOAT32, (32,))) == 1
+    # valid calls reach the device check
+    assert _linear(res32, x, w, s, b, A(_lib.BFLOAT16, (32,))) == 4
+    assert _linear(A(_lib.FLOAT16, (1, 32)), xs, w, s, b, A(_lib.FLOAT16, (32,))) == 4
+    assert _linear(res, x, w, s, b, None) == 4
+
+
+def test_mlp_gate_up_validation():
+    res, x, w, s, b = good()
+    L = _lib.lib()
+
+    def call(act, bg=None, bu=None, r=res):
+        return L.kh_mlp_gate_up(ctypes.byref(r), ctypes.byref(x), ctypes.byref(w), ctypes.byref(s),
+                                ctypes.byref(b), None if bg is None else ctypes.byref(bg), ctypes.byref(w),
+                                ctypes.byref(s), ctypes.byref(b), None if bu is None else ctypes.byref(bu),
+                                act, _lib.opt(64), _lib.opt(4), b"affine", None)
+    assert call(7) == 1 and "activation 7" in _lib.last_error()
+    assert call(_lib.ACT_GELU_APPROX, bu=A(_lib.FLOAT32, (33,))) == 1
+    assert "bias_up" in _lib.last_error()
+    assert call(_lib.ACT_GELU_APPROX) == 4
+    assert call(_lib.ACT_SILU, A(_lib.FLOAT32, (32,)), A(_lib.FLOAT32, (32,)), A(_lib.FLOAT32, (1, 32))) == 4
+
+
+def test_linear_multi_validation():
+    res, x, w, s, b = good()
+    L = _lib.lib()
+    P = ctypes.POINTER(_lib.KhArray)
+    arr = lambda *a: (P * len(a))(*[ctypes.pointer(v) if v is not None else P() for v in a])
+    res32 = A(_lib.FLOAT32, (1, 32))
+    call = lambda r, bias: L.kh_linear_multi(2, arr(r, r), ctypes.byref(x), arr(w, w), arr(s, s), arr(b, b),
+                                             bias, _lib.opt(64), _lib.opt(4), b"affine", None)
+    assert call(res32, arr(A(_lib.FLOAT32, (32,)), A(_lib.FLOAT32, (31,)))) == 1
+    assert "(31)" in _lib.last_error()
+    assert call(res32, arr(None, A(_lib.FLOAT32, (32,)))) == 4
+    assert call(res, None) == 4

@@ -1,7 +1,7 @@
 """The C++ host layer (kiln_amd/host, driven by tests/cpp/kiln_host_run.cpp):
 safetensors loading (single file and sharded index, weights.rs:45-106),
 config validation (config.rs:137-148, 735-760), Linear (nn.rs:51-114) with
-its bias add, Embedding lookup and tied head (nn.rs:116-194), and the row
+its bias add, the gated Mlp (nn.rs:259-294, silu and gelu_approx), Embedding lookup and tied head (nn.rs:116-194), and the row
 stability probe (nn.rs:301-327) — checked against the CPU oracle."""
 import json
 import os
@@ -182,3 +182,51 @@ def test_switch_linear_from_checkpoint(oracle, tmp_path, form, P):
                                       gs, 4, True, "f16")
         ref = (oracle.to_f32(r16, "f16") + bias[e].astype(np.float32)).astype(np.float16).astype(np.float64)[0]
         assert np.max(np.abs(y[p] - ref)) <= 2e-2 * np.max(np.abs(ref)), p
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("act", ["silu", "gelu_approx"])
+@pytest.mark.parametrize("M", [1, 40])
+def test_mlp_from_checkpoint(oracle, tmp_path, act, M):
+    """nn::Mlp (nn.rs:259-294): down(act(gate(x) + b_g) * (up(x) + b_u)) + b_d
+    with mlp_bias-style biases, the gate/up half in one kh_mlp_gate_up call;
+    against the oracle's per-op composition (Linear::forward = matmul then
+    bias; the activation with every intermediate in float16)."""
+    from safetensors.numpy import save_file
+    H, I, gs = 256, 192, 64
+    pre = "model.layers.0.mlp"
+    Ls = {p: make_linear_numpy(n, k, gs, "q4", seed=70 + i) for i, (p, n, k) in
+          enumerate((("gate_proj", I, H), ("up_proj", I, H), ("down_proj", H, I)))}
+    rng = np.random.default_rng(74)
+    bias = {p: (rng.standard_normal(n) * 0.1).astype(np.float16) for p, n in
+            (("gate_proj", I), ("up_proj", I), ("down_proj", H))}
+    t = {}
+    for p, L in Ls.items():
+        t[f"{pre}.{p}.weight"] = L["w"]
+        t[f"{pre}.{p}.scales"] = L["scales"].view(np.float16)
+        t[f"{pre}.{p}.biases"] = L["biases"].view(np.float16)
+        t[f"{pre}.{p}.bias"] = bias[p]
+    d = tmp_path / "mlp"
+    d.mkdir()
+    save_file(t, str(d / "model.safetensors"))
+    (d / "config.json").write_text(json.dumps({"model_type": "gemma2",
+                                               "quantization": {"group_size": gs, "bits": 4}}))
+    x = make_x_numpy(M, H, seed=75, xdt="f16")
+    (tmp_path / "x.bin").write_bytes(x.tobytes())
+    rc, out, err = _job(tmp_path, model_dir=str(d), op="mlp", prefix=pre, activation=act,
+                        input=str(tmp_path / "x.bin"), input_shape=[1, M, H], input_dtype="float16",
+                        output=str(tmp_path / "y.bin"))
+    assert rc == 0 and out["ok"], (out, err)
+    assert out["shape"] == [1, M, H] and out["dtype"] == "float16"
+    y = np.frombuffer((tmp_path / "y.bin").read_bytes(), dtype=np.uint16).reshape(M, H)
+
+    def lin(p, v):
+        L = Ls[p]
+        r, _ = oracle.linear(v, "f16", L["w"], L["scales"], L["biases"], "f16", gs, 4,
+                             bias[p].view(np.uint16), "f16")
+        return r
+    fn = oracle.gelu_mul if act == "gelu_approx" else oracle.silu_mul
+    ref = lin("down_proj", fn(lin("gate_proj", x), lin("up_proj", x), "f16"))
+    yf, rf = oracle.to_f32(y, "f16").astype(np.float64), oracle.to_f32(ref, "f16").astype(np.float64)
+    assert np.max(np.abs(yf - rf)) <= 2e-2 * np.max(np.abs(rf))
+    assert np.mean(np.abs(yf - rf)) <= 1e-3 * np.mean(np.abs(rf))

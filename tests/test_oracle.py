@@ -242,6 +242,67 @@ def test_silu_mul_special_values_and_rounding(oracle, dt):
     assert np.array_equal(oracle.from_f32(got, dt), oracle.silu_mul(g, u, dt))
 
 
+def test_gelu_mul_f32_is_the_closed_form(oracle):
+    """In float32 the per-op roundings are float32's own: the result is the
+    tanh approximation of GELU (0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3))),
+    evaluated here in float64) times up, to float32 accuracy; torch's tanh-GELU
+    agrees. A wrong constant, sign or missing term fails by far more."""
+    rng = np.random.default_rng(6)
+    g = (rng.standard_normal(4096) * 4).astype(np.float32)
+    u = rng.standard_normal(4096).astype(np.float32)
+    got = oracle.gelu_mul(g, u, "f32").astype(np.float64)
+    gd = g.astype(np.float64)
+    want = 0.5 * gd * (1 + np.tanh(np.sqrt(2 / np.pi) * (gd + 0.044715 * gd ** 3))) * u
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+    import torch
+    t = (torch.nn.functional.gelu(torch.from_numpy(g), approximate="tanh") * torch.from_numpy(u)).numpy()
+    assert np.allclose(got, t, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_gelu_mul_special_values_and_rounding(oracle, dt):
+    g = oracle.from_f32(np.array([0.0, 8.0, -8.0, 1.0, -1.0, 2.0], np.float32), dt)
+    u = oracle.from_f32(np.ones(6, np.float32), dt)
+    got = oracle.to_f32(oracle.gelu_mul(g, u, dt), dt)
+    assert got[0] == 0                # gelu(0) = 0
+    assert got[1] == 8.0              # tanh saturates: gate rounds to 2, act = x
+    assert abs(got[2]) < 2e-2         # gelu(-8) ~ 0 (the gate 1 + tanh rounds in dt)
+    # gelu(1) = 0.8411920, gelu(-1) = -0.1588080, gelu(2) = 1.9545977, within
+    # the per-op roundings of dt
+    for i, v in ((3, 0.8411920), (4, -0.1588080), (5, 1.9545977)):
+        assert abs(got[i] - v) <= 2 ** (-8 if dt == "bf16" else -11) * 16 * max(abs(v), 1)
+    assert np.array_equal(oracle.from_f32(got, dt), oracle.gelu_mul(g, u, dt))
+    # the reference rounds every intermediate: with dt = bf16 the result
+    # differs from the float32 evaluation rounded once somewhere in a sweep
+    if dt == "bf16":
+        xs = oracle.from_f32(np.linspace(-4, 4, 801).astype(np.float32), dt)
+        once = oracle.from_f32(oracle.gelu_mul(oracle.to_f32(xs, dt), np.ones(801, np.float32), "f32"), dt)
+        assert not np.array_equal(oracle.gelu_mul(xs, oracle.from_f32(np.ones(801, np.float32), dt), dt), once)
+
+
+def test_linear_rounds_the_product_then_adds(oracle):
+    """Linear::forward (nn.rs:79-102) is two arrays: the product in its own
+    dtype, then + bias. The oracle's linear equals quantized_matmul rounded to
+    the product's dtype followed by the float32 sum rounded to the result's."""
+    from kiln_amd.workloads import make_linear_numpy, make_x_numpy
+    L = make_linear_numpy(48, 256, 64, "q4", seed=3, sdt="bf16")
+    x = make_x_numpy(5, 256, seed=4)
+    bias = oracle.from_f32(np.random.default_rng(1).standard_normal(48).astype(np.float32), "bf16")
+    y, ydt = oracle.linear(x, "bf16", L["w"], L["scales"], L["biases"], "bf16", 64, 4)
+    assert ydt == "bf16"
+    r, rdt = oracle.linear(x, "bf16", L["w"], L["scales"], L["biases"], "bf16", 64, 4, bias, "bf16")
+    assert rdt == "bf16"
+    assert np.array_equal(r, oracle.from_f32(oracle.to_f32(y, "bf16") + oracle.to_f32(bias, "bf16"), "bf16"))
+    r32, rdt = oracle.linear(x, "bf16", L["w"], L["scales"], L["biases"], "bf16", 64, 4,
+                             oracle.to_f32(bias, "bf16"), "f32")
+    assert rdt == "f32"   # bf16 product + f32 bias -> f32, the product still rounded to bf16 first
+    assert np.array_equal(r32, oracle.to_f32(y, "bf16") + oracle.to_f32(bias, "bf16"))
+    # against float64: within the product's rounding plus the sum's
+    exact = oracle.np_qmm_f64(x, "bf16", L["w"], L["scales"], L["biases"], "bf16", 64, 4) + \
+        oracle.to_f32(bias, "bf16").astype(np.float64)
+    assert np.allclose(oracle.to_f32(r, "bf16"), exact, rtol=2 ** -7, atol=2e-2)
+
+
 # --------------------------------------------------------------------------- affine quantize
 
 def _dq_f32(oracle, wq, s, b, dt, gs, bits):
