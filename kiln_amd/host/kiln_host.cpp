@@ -2,12 +2,18 @@
 #include "kiln_host.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
 #include <mutex>
 #include <set>
 #include <sstream>
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 namespace kiln {
 
@@ -195,6 +201,15 @@ Result<Array> Array::empty(const std::vector<int64_t>& shape, Dtype dtype, const
   a.shape_ = shape;
   a.dtype_ = dtype;
   a.stream_ = s.raw();
+  // element count with overflow checks: no shape may ask for more than 2^48 bytes
+  uint64_t n = 1;
+  for (int64_t d : shape) {
+    if (d < 0) return Error{"array shape has a negative dimension"};
+    if (d != 0 && n > (uint64_t(1) << 48) / (uint64_t)d) return Error{"array shape is too large"};
+    n *= (uint64_t)d;
+  }
+  if (n > (uint64_t(1) << 48) / (uint64_t)std::max<size_t>(dtype_size(dtype), 1))
+    return Error{"array shape is too large"};
   const size_t bytes = a.nbytes();
   if (bytes > 0) {
     auto p = Allocator::get().alloc(bytes, s.raw(), &a.cap_);
@@ -436,7 +451,160 @@ Result<Dtype> safetensors_dtype(const std::string& name, const std::string& t) {
   return Error{"tensor " + name + " has unsupported dtype " + t};
 }
 
+// A JSON number that is an integer in [0, 2^53].
+bool as_count(const json::Value& v, uint64_t* out) {
+  if (v.kind != json::Value::Number || !(v.num >= 0) || v.num > 9007199254740992.0 || std::floor(v.num) != v.num)
+    return false;
+  *out = (uint64_t)v.num;
+  return true;
+}
+
+// A read-only private mapping of a whole file, unmapped on destruction.
+class MappedFile {
+ public:
+  static Result<MappedFile> open(const std::string& path) {
+    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return Error{"failed to read " + path + ": cannot open"};
+    struct stat st;
+    if (fstat(fd, &st) != 0) {
+      ::close(fd);
+      return Error{"failed to read " + path + ": cannot stat"};
+    }
+    MappedFile m;
+    m.size_ = (size_t)st.st_size;
+    if (m.size_ > 0) {
+      void* p = mmap(nullptr, m.size_, PROT_READ, MAP_PRIVATE, fd, 0);
+      if (p == MAP_FAILED) {
+        ::close(fd);
+        return Error{"failed to map " + path};
+      }
+      m.data_ = static_cast<const unsigned char*>(p);
+      (void)madvise(p, m.size_, MADV_SEQUENTIAL);
+    }
+    ::close(fd);
+    return m;
+  }
+  MappedFile() = default;
+  MappedFile(MappedFile&& o) noexcept : data_(o.data_), size_(o.size_) { o.data_ = nullptr, o.size_ = 0; }
+  MappedFile& operator=(MappedFile&& o) noexcept {
+    std::swap(data_, o.data_);
+    std::swap(size_, o.size_);
+    return *this;
+  }
+  MappedFile(const MappedFile&) = delete;
+  ~MappedFile() {
+    if (data_) munmap(const_cast<unsigned char*>(data_), size_);
+  }
+  const unsigned char* data() const { return data_; }
+  size_t size() const { return size_; }
+  // Give back the pages wholly inside [from, to) (they are re-read from the
+  // file if touched again).
+  void release(size_t from, size_t to) const {
+    const size_t pg = (size_t)sysconf(_SC_PAGESIZE);
+    const size_t a = (from + pg - 1) / pg * pg, b = to / pg * pg;
+    if (data_ && b > a) (void)madvise(const_cast<unsigned char*>(data_) + a, b - a, MADV_DONTNEED);
+  }
+
+ private:
+  const unsigned char* data_ = nullptr;
+  size_t size_ = 0;
+};
+
+// Host -> device copies through two pinned buffers of kStageBytes each: a
+// chunk is copied from the mapping into a free buffer, sent asynchronously,
+// and the buffer is reused once its event has completed.
+class StagedUpload {
+ public:
+  static constexpr size_t kStageBytes = size_t(32) << 20;
+  ~StagedUpload() {
+    for (int i = 0; i < 2; ++i) {
+      if (ev_[i]) (void)hipEventSynchronize(ev_[i]), (void)hipEventDestroy(ev_[i]);
+      if (buf_[i]) (void)hipHostFree(buf_[i]);
+    }
+  }
+  Result<void> init() {
+    for (int i = 0; i < 2; ++i) {
+      hipError_t e = hipHostMalloc(&buf_[i], kStageBytes, hipHostMallocDefault);
+      if (e == hipSuccess) e = hipEventCreateWithFlags(&ev_[i], hipEventDisableTiming);
+      if (e != hipSuccess) return hip_error("pinned staging buffer", e);
+    }
+    return {};
+  }
+  // Copies file bytes [off, off + n) to dst on stream s, releasing the pages.
+  Result<void> copy(const MappedFile& f, size_t off, size_t n, void* dst, hipStream_t s) {
+    size_t done = 0;
+    while (done < n) {
+      const size_t c = std::min(kStageBytes, n - done);
+      hipError_t e = hipEventSynchronize(ev_[cur_]);  // this buffer's previous copy has finished
+      if (e != hipSuccess) return hip_error("staging copy", e);
+      std::memcpy(buf_[cur_], f.data() + off + done, c);
+      f.release(off + done, off + done + c);
+      e = hipMemcpyAsync(static_cast<char*>(dst) + done, buf_[cur_], c, hipMemcpyHostToDevice, s);
+      if (e == hipSuccess) e = hipEventRecord(ev_[cur_], s);
+      if (e != hipSuccess) return hip_error("staging copy", e);
+      cur_ ^= 1;
+      done += c;
+    }
+    return {};
+  }
+
+ private:
+  void* buf_[2] = {nullptr, nullptr};
+  hipEvent_t ev_[2] = {nullptr, nullptr};
+  int cur_ = 0;
+};
+
 }  // namespace
+
+Result<std::vector<SafetensorsEntry>> read_safetensors_header(const void* data, size_t size,
+                                                              const std::string& path) {
+  const auto bad = [&](const std::string& what) { return Error{"invalid safetensors file " + path + ": " + what}; };
+  if (size < 8) return bad("too short");
+  uint64_t hlen = 0;
+  std::memcpy(&hlen, data, 8);  // little-endian u64 header length
+  if (hlen > size - 8 || hlen > (uint64_t(100) << 20)) return bad("header length");
+  json::Value header;
+  try {
+    header = json::parse(std::string(static_cast<const char*>(data) + 8, (size_t)hlen));
+  } catch (const std::exception& e) {
+    return bad(e.what());
+  }
+  if (!header.is_object()) return bad("header is not an object");
+  const uint64_t avail = size - 8 - hlen;
+  std::vector<SafetensorsEntry> out;
+  for (const auto& kv : header.obj) {
+    if (kv.first == "__metadata__") continue;
+    const json::Value& t = kv.second;
+    const json::Value* dt = t.get("dtype");
+    const json::Value* sh = t.get("shape");
+    const json::Value* off = t.get("data_offsets");
+    if (!dt || !dt->is_string() || !sh || !sh->is_array() || !off || !off->is_array() || off->arr.size() != 2)
+      return bad("bad entry " + kv.first);
+    auto dtype = safetensors_dtype(kv.first, dt->str);
+    if (!dtype) return dtype.error();
+    if (sh->arr.size() > KH_MAX_NDIM) return bad("rank of " + kv.first);
+    SafetensorsEntry e;
+    e.name = kv.first;
+    e.dtype = dtype.value();
+    uint64_t count = 1;
+    for (const auto& d : sh->arr) {
+      uint64_t v;
+      if (!as_count(d, &v)) return bad("shape of " + kv.first);
+      if (v != 0 && count > (uint64_t(1) << 48) / v) return bad("shape of " + kv.first);
+      count *= v;
+      e.shape.push_back((int64_t)v);
+    }
+    uint64_t o0, o1;
+    if (!as_count(off->arr[0], &o0) || !as_count(off->arr[1], &o1) || o1 < o0 || o1 > avail)
+      return bad("data offsets of " + kv.first);
+    if (count * (uint64_t)dtype_size(e.dtype) != o1 - o0)
+      return bad("data offsets of " + kv.first + " do not match its shape");
+    e.offset = o0;
+    e.nbytes = o1 - o0;
+    out.push_back(std::move(e));
+  }
+  return out;
+}
 
 Result<WeightStore> WeightStore::from_model_dir(const std::string& dir, const Stream& s) {
   std::set<std::string> files;
@@ -461,42 +629,36 @@ Result<WeightStore> WeightStore::from_model_dir(const std::string& dir, const St
     }
   }
   WeightStore store;
+  StagedUpload up;
+  bool staged = false;
   for (const std::string& file : files) {
     const std::string path = dir + "/" + file;
-    auto blob = read_file(path);
-    if (!blob) return blob.error();
-    const std::string& b = blob.value();
-    if (b.size() < 8) return Error{"invalid safetensors file " + path + ": too short"};
+    auto mf = MappedFile::open(path);
+    if (!mf) return mf.error();
+    const MappedFile& m = mf.value();
+    auto entries = read_safetensors_header(m.data(), m.size(), path);
+    if (!entries) return entries.error();
     uint64_t hlen = 0;
-    std::memcpy(&hlen, b.data(), 8);  // little-endian u64 header length
-    if (hlen > b.size() - 8) return Error{"invalid safetensors file " + path + ": header length"};
-    json::Value header;
-    try {
-      header = json::parse(b.substr(8, (size_t)hlen));
-    } catch (const std::exception& e) {
-      return Error{"invalid safetensors file " + path + ": " + e.what()};
-    }
-    if (!header.is_object()) return Error{"invalid safetensors file " + path + ": header is not an object"};
+    std::memcpy(&hlen, m.data(), 8);
     const size_t base = 8 + (size_t)hlen;
-    for (const auto& kv : header.obj) {
-      if (kv.first == "__metadata__") continue;
-      const json::Value& t = kv.second;
-      const json::Value* dt = t.get("dtype");
-      const json::Value* sh = t.get("shape");
-      const json::Value* off = t.get("data_offsets");
-      if (!dt || !dt->is_string() || !sh || !sh->is_array() || !off || !off->is_array() || off->arr.size() != 2)
-        return Error{"invalid safetensors file " + path + ": bad entry " + kv.first};
-      auto dtype = safetensors_dtype(kv.first, dt->str);
-      if (!dtype) return dtype.error();
-      std::vector<int64_t> shape;
-      for (const auto& d : sh->arr) shape.push_back((int64_t)d.num);
-      const size_t o0 = (size_t)off->arr[0].num, o1 = (size_t)off->arr[1].num;
-      if (o1 < o0 || base + o1 > b.size())
-        return Error{"invalid safetensors file " + path + ": data offsets of " + kv.first};
-      auto arr = Array::from_bytes(b.data() + base + o0, o1 - o0, shape, dtype.value(), s);
-      if (!arr) return Error{"tensor " + kv.first + ": " + arr.error().message};
-      store.tensors_[kv.first] = arr.take();
+    for (const SafetensorsEntry& e : entries.value()) {
+      auto r = Array::empty(e.shape, e.dtype, s);
+      if (!r) return Error{"tensor " + e.name + ": " + r.error().message};
+      Array arr = r.take();
+      if (e.nbytes) {
+        if (!staged) {
+          auto ok = up.init();
+          if (!ok) return ok.error();
+          staged = true;
+        }
+        auto ok = up.copy(m, base + e.offset, e.nbytes, arr.data(), s.raw());
+        if (!ok) return Error{"tensor " + e.name + ": " + ok.error().message};
+      }
+      store.tensors_[e.name] = std::move(arr);
     }
+    // the mapping is dropped at the end of this iteration: finish its copies
+    const hipError_t err = hipStreamSynchronize(s.raw());
+    if (err != hipSuccess) return hip_error("checkpoint upload", err);
   }
   return store;
 }

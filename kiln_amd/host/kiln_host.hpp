@@ -183,8 +183,27 @@ Result<Array> linear(const Array& x, const Array& w, const Array& scales, const 
                      const std::optional<Array>& bias, int group_size, int bits, const Stream& s);
 }  // namespace ops
 
+// One tensor of a safetensors file: dtype, shape and its byte range within
+// the data section (after the 8-byte length and the JSON header).
+struct SafetensorsEntry {
+  std::string name;
+  Dtype dtype;
+  std::vector<int64_t> shape;
+  uint64_t offset = 0, nbytes = 0;
+};
+// Parses and validates the header of a safetensors file held in `data`
+// (`size` bytes): dtypes, non-negative integral dims whose element count
+// times the element size equals the entry's byte range, and byte ranges
+// inside the file. Malformed input is an error, never a huge allocation.
+Result<std::vector<SafetensorsEntry>> read_safetensors_header(const void* data, size_t size,
+                                                              const std::string& path);
+
 // safetensors checkpoint store: weights.rs:37-130 (single file or sharded
-// through model.safetensors.index.json; F16/BF16/F32/U32/I32 tensors).
+// through model.safetensors.index.json; F16/BF16/F32/U32/I32 tensors). Each
+// file is memory-mapped read-only (as weights.rs:76 maps it through
+// MappedFile, io.rs:22-30) and copied to the device through a bounded pinned
+// staging buffer; pages already copied are released, so the host memory a
+// load holds stays near the staging buffer's size.
 class WeightStore {
  public:
   static Result<WeightStore> from_model_dir(const std::string& dir, const Stream& s);

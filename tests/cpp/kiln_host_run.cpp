@@ -5,7 +5,7 @@
 //   kiln_host_run job <job.json>      loads a checkpoint directory and runs one
 //                                     layer call on the GPU, writing raw output
 //
-// job.json: {"model_dir": d, "op": "linear"|"mlp"|"embed"|"as_linear"|"probe"|"load"|"switch",
+// job.json: {"model_dir": d, "op": "linear"|"mlp"|"embed"|"as_linear"|"probe"|"load"|"load_all"|"switch",
 //            "prefix": p, "input": file, "input_shape": [...],
 //            "input_dtype": "bfloat16"|"float16"|"float32"|"uint32"|"int32",
 //            "output": file}
@@ -13,7 +13,9 @@
 // {"ok": false, "error": "..."}; "probe" prints {"ok": true, "m": first
 // divergent M}; "load" prints the linear's io_features and remaining tensors.
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <vector>
 #include <fstream>
 #include <iostream>
 #include <sstream>
@@ -86,6 +88,36 @@ static int selftest() {
   // dtype sizes
   CHECK(dtype_size(Dtype::Bfloat16) == 2 && dtype_size(Dtype::Uint32) == 4);
 
+  // safetensors header validation: malformed headers are errors
+  auto st_file = [](const std::string& header, size_t data_bytes) {
+    std::string f(8, '\0');
+    const uint64_t n = header.size();
+    std::memcpy(&f[0], &n, 8);
+    return f + header + std::string(data_bytes, '\x01');
+  };
+  auto hdr = [&](const std::string& h, size_t data_bytes) {
+    const std::string f = st_file(h, data_bytes);
+    return read_safetensors_header(f.data(), f.size(), "t.safetensors");
+  };
+  auto okh = hdr(R"({"a": {"dtype": "F16", "shape": [2, 3], "data_offsets": [0, 12]}, "__metadata__": {}})", 12);
+  CHECK(okh.ok() && okh.value().size() == 1 && okh.value()[0].nbytes == 12 && okh.value()[0].shape[1] == 3);
+  CHECK(!hdr(R"({"a": {"dtype": "F16", "shape": [-2, 3], "data_offsets": [0, 12]}})", 12).ok());
+  CHECK(!hdr(R"({"a": {"dtype": "F16", "shape": [2.5, 3], "data_offsets": [0, 12]}})", 12).ok());
+  CHECK(!hdr(R"({"a": {"dtype": "F16", "shape": [4294967296, 4294967296, 4294967296], "data_offsets": [0, 12]}})", 12).ok());
+  CHECK(!hdr(R"({"a": {"dtype": "F16", "shape": [2, 3], "data_offsets": [0, 14]}})", 14).ok());   // shape mismatch
+  CHECK(!hdr(R"({"a": {"dtype": "F16", "shape": [2, 3], "data_offsets": [0, 12]}})", 8).ok());    // past the end
+  CHECK(!hdr(R"({"a": {"dtype": "F16", "shape": [2, 3], "data_offsets": [12, 0]}})", 12).ok());
+  CHECK(!hdr(R"({"a": {"dtype": "F16", "shape": [2, 3], "data_offsets": [-1e300, 12]}})", 12).ok());
+  CHECK(!hdr(R"({"a": {"dtype": "F64", "shape": [1], "data_offsets": [0, 8]}})", 8).ok());
+  {
+    std::string f = st_file("{}", 0);
+    const uint64_t huge = ~uint64_t(0) - 3;
+    std::memcpy(&f[0], &huge, 8);
+    CHECK(!read_safetensors_header(f.data(), f.size(), "t").ok());
+  }
+  // an array too large for any device is an error, not a hang
+  CHECK(!Array::empty({int64_t(1) << 40, int64_t(1) << 20}, Dtype::Float32, Stream::gpu()).ok());
+
   std::printf("{\"ok\": %s, \"failures\": %d}\n", fails ? "false" : "true", fails);
   return fails ? 1 : 0;
 }
@@ -96,6 +128,15 @@ static Dtype parse_dtype(const std::string& s) {
   if (s == "float32") return Dtype::Float32;
   if (s == "uint32") return Dtype::Uint32;
   return Dtype::Int32;
+}
+
+// A field of /proc/self/status in KiB (VmRSS: resident now; VmHWM: peak).
+static long proc_kib(const char* key) {
+  std::ifstream f("/proc/self/status");
+  std::string line;
+  while (std::getline(f, line))
+    if (line.compare(0, std::strlen(key), key) == 0) return std::atol(line.c_str() + std::strlen(key));
+  return -1;
 }
 
 static int fail_json(const std::string& msg) {
@@ -116,8 +157,32 @@ static int job(const std::string& path) {
   cs << cf.rdbuf();
   auto quant = quantization_from_config(json::parse(cs.str()));
   if (!quant) return fail_json(quant.error().message);
+  if (op == "load_all") (void)hipFree(nullptr);  // the runtime is up before memory is measured
+  const long rss_before = proc_kib("VmRSS:");
   auto store = WeightStore::from_model_dir(dir, s);
   if (!store) return fail_json(store.error().message);
+  if (op == "load_all") {  // the whole store: host memory around the load, and
+                           // FNV-1a hashes of each tensor's first and last 4 KiB
+    const long hwm_after = proc_kib("VmHWM:");
+    std::string hs = "{";
+    for (const auto& name : store.value().remaining()) {
+      auto t = store.value().take(name);
+      if (!t) return fail_json(t.error().message);
+      const Array& a = t.value();
+      const size_t n = a.nbytes(), k = n < 4096 ? n : 4096;
+      std::vector<unsigned char> h(2 * k);
+      if (k && (hipMemcpy(h.data(), a.data(), k, hipMemcpyDeviceToHost) != hipSuccess ||
+                hipMemcpy(h.data() + k, static_cast<const char*>(a.data()) + n - k, k, hipMemcpyDeviceToHost) !=
+                    hipSuccess))
+        return fail_json("readback of " + name);
+      uint64_t f = 1469598103934665603ull;
+      for (unsigned char c : h) f = (f ^ c) * 1099511628211ull;
+      hs += (hs.size() > 1 ? ", " : "") + jstr(name) + ": " + jstr(std::to_string(f));
+    }
+    std::printf("{\"ok\": true, \"rss_before_kib\": %ld, \"hwm_after_kib\": %ld, \"hashes\": %s}}\n",
+                rss_before, hwm_after, hs.c_str());
+    return 0;
+  }
 
   if (op == "load") {
     auto l = nn::Linear::load(store.value(), prefix, quant.value());
