@@ -252,9 +252,10 @@ int kh_quantized_embedding(kh_array* res, const kh_array* ids,
                            kh_optional_int bits, const char* mode,
                            kh_stream stream);
 
-/* res = a + b, elementwise, with b broadcast over a's leading dimensions
- * (b.shape == a.shape[a.ndim - b.ndim:]). a, b, res: bfloat16|float16|float32;
- * res has a's shape. Each sum is formed in float32 and rounded once to res. */
+/* res = a + b, elementwise, with numpy broadcasting (dimensions aligned from
+ * the right; a dimension of size 1 stretches), as mlx_add. a, b, res:
+ * bfloat16|float16|float32; res has the broadcast shape. Each sum is formed in
+ * float32 and rounded once to res. */
 int kh_add(kh_array* res, const kh_array* a, const kh_array* b, kh_stream stream);
 
 /* kh_quantized_matmul without any device allocation. No counterpart in the

@@ -168,6 +168,22 @@ __global__ void add_kernel(const void* __restrict__ a, int adt, const void* __re
   store_from_f32(res, rdt, i, load_as_f32(a, adt, i) + load_as_f32(b, bdt, i % nb));
 }
 
+// General broadcasting: element i of the result at coordinates over `shape`
+// reads a and b through their strides (0 along broadcast dimensions).
+__global__ void add_bcast_kernel(const void* __restrict__ a, int adt, const void* __restrict__ b, int bdt,
+                                 void* __restrict__ res, int rdt, int64_t n, AddShape sh) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int64_t ia = 0, ib = 0, rem = i;
+  for (int d = sh.nd - 1; d >= 0; --d) {
+    const int64_t c = rem % sh.shape[d];
+    rem /= sh.shape[d];
+    ia += c * sh.as[d];
+    ib += c * sh.bs[d];
+  }
+  store_from_f32(res, rdt, i, load_as_f32(a, adt, ia) + load_as_f32(b, bdt, ib));
+}
+
 // gather_qmm, any dtype / alignment / M: one thread per output column n,
 // pairs x rows over grid.y; float32 fma chain in k order (as the oracle).
 template <int BITS>
@@ -305,6 +321,14 @@ hipError_t launch_add(const void* a, int adt, const void* b, int bdt, void* res,
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, a, adt, b, bdt, res,
                      rdt, n, nb);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_bcast(const void* a, int adt, const void* b, int bdt, void* res, int rdt, int64_t n,
+                            const AddShape& sh, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(add_bcast_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, a, adt, b, bdt, res,
+                     rdt, n, sh);
   return hipGetLastError();
 }
 

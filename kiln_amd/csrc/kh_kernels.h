@@ -178,6 +178,15 @@ hipError_t launch_act_mul(const void* g, const void* u, void* res, int dt, int64
 hipError_t launch_add(const void* a, int adt, const void* b, int bdt, void* res, int rdt, int64_t n,
                       int64_t nb, hipStream_t stream);
 
+// res = a + b with numpy broadcasting: res has `shape` (nd dims); a and b are
+// read with element strides as / bs (0 along their broadcast dimensions).
+struct AddShape {
+  int nd;
+  int64_t shape[8], as[8], bs[8];
+};
+hipError_t launch_add_bcast(const void* a, int adt, const void* b, int bdt, void* res, int rdt, int64_t n,
+                            const AddShape& sh, hipStream_t stream);
+
 // take(a, ids, axis=0) on rows of row_bytes bytes.
 hipError_t launch_take(const void* a, int64_t V, int64_t row_bytes, const void* ids,
                        bool ids_signed, int64_t T, void* out, hipStream_t stream);

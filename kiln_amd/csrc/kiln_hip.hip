@@ -902,21 +902,39 @@ int kh_add(kh_array* res, const kh_array* a, const kh_array* b, kh_stream stream
   if (!is_float(a->dtype) || !is_float(b->dtype))
     return fail(KH_ERR_INVALID_ARGUMENT, "[%s] operands must be float16/bfloat16/float32, got %s and %s",
                 op, dtype_name(a->dtype), dtype_name(b->dtype));
-  if (b->ndim > a->ndim)
-    return fail(KH_ERR_INVALID_ARGUMENT, "[%s] cannot broadcast %s onto %s", op, shape_str(b).c_str(),
-                shape_str(a).c_str());
-  for (int i = 0; i < b->ndim; ++i)
-    if (b->shape[i] != a->shape[a->ndim - b->ndim + i])
-      return fail(KH_ERR_INVALID_ARGUMENT, "[%s] cannot broadcast %s onto %s", op, shape_str(b).c_str(),
-                  shape_str(a).c_str());
-  kh_array want = *a;
+  // numpy broadcasting, dimensions aligned from the right
+  const int nd = a->ndim > b->ndim ? a->ndim : b->ndim;
+  kh_array want{};
+  want.dtype = res ? res->dtype : 0;
+  want.ndim = nd;
+  kh::AddShape sh{};
+  sh.nd = nd;
+  int64_t sa = 1, sb = 1;
+  bool suffix = b->ndim <= a->ndim;  // b.shape == a.shape[-b.ndim:]: the plain kernel
+  for (int d = nd - 1; d >= 0; --d) {
+    const int da = d - (nd - a->ndim), db = d - (nd - b->ndim);
+    const int64_t ea = da >= 0 ? a->shape[da] : 1, eb = db >= 0 ? b->shape[db] : 1;
+    if (ea != eb && ea != 1 && eb != 1)
+      return fail(KH_ERR_INVALID_ARGUMENT, "[%s] cannot broadcast %s with %s", op, shape_str(a).c_str(),
+                  shape_str(b).c_str());
+    const int64_t e = ea == 1 ? eb : ea;
+    want.shape[d] = e;
+    sh.shape[d] = e;
+    sh.as[d] = ea == 1 ? 0 : sa;
+    sh.bs[d] = eb == 1 ? 0 : sb;
+    if (db >= 0 && eb != ea) suffix = false;
+    if (da >= 0) sa *= ea;
+    if (db >= 0) sb *= eb;
+  }
   if ((rc = check_result(op, res, want))) return rc;
-  const int64_t n = numel(a), nb = numel(b);
+  const int64_t n = numel(&want), nb = numel(b);
   if (n == 0) return KH_OK;
-  if (nb == 0) return fail(KH_ERR_INVALID_ARGUMENT, "[%s] empty addend for non-empty array", op);
   if ((rc = check_device(op))) return rc;
-  hipError_t e = kh::launch_add(a->data, a->dtype, b->data, b->dtype, res->data, res->dtype, n, nb,
-                                static_cast<hipStream_t>(stream));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const hipError_t e = suffix ? kh::launch_add(a->data, a->dtype, b->data, b->dtype, res->data, res->dtype, n,
+                                               nb, st)
+                              : kh::launch_add_bcast(a->data, a->dtype, b->data, b->dtype, res->data,
+                                                     res->dtype, n, sh, st);
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
 }
 

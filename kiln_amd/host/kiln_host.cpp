@@ -399,7 +399,14 @@ Result<Array> quantized_embedding(const Array& ids, const Array& w, const Array&
 }
 
 Result<Array> add(const Array& a, const Array& b, const Stream& s) {
-  auto r = Array::empty(a.shape(), promote(a.dtype(), b.dtype()), s);
+  const int nd = std::max(a.ndim(), b.ndim());
+  std::vector<int64_t> shape(nd);
+  for (int d = 0; d < nd; ++d) {  // numpy broadcasting; the library checks compatibility
+    const int da = d - (nd - a.ndim()), db = d - (nd - b.ndim());
+    const int64_t ea = da >= 0 ? a.dim(da) : 1, eb = db >= 0 ? b.dim(db) : 1;
+    shape[d] = ea == 1 ? eb : ea;
+  }
+  auto r = Array::empty(shape, promote(a.dtype(), b.dtype()), s);
   if (!r) return r;
   Array out = r.take();
   kh_array res = out.desc(), ad = a.desc(), bd = b.desc();
@@ -870,12 +877,13 @@ Result<Array> SwitchLinear::forward(const Array& x, const Array& indices, bool s
                                     const Stream& s) const {
   auto y = ops::gather_qmm(x, weight_, scales_, biases_, indices, true, group_size_, bits_, sorted_indices, s);
   if (!y || !bias_) return y;
-  // y + expand_dims(bias[indices], -2): bias rows gathered to indices.shape + [N]
-  if (y.value().dim(-2) != 1 || y.value().ndim() != indices.ndim() + 2)
-    return Error{"[SwitchLinear] an expert bias needs one row per batch pair"};
+  // y + expand_dims(bias[indices], -2): bias rows gathered to indices.shape +
+  // [1, N], broadcast against y [batch..., M, N]
   auto g = ops::take(*bias_, indices, 0, s);
   if (!g) return g;
-  auto gv = g.value().view(y.value().shape());
+  std::vector<int64_t> shape = g.value().shape();
+  shape.insert(shape.end() - 1, 1);
+  auto gv = g.value().view(shape);
   if (!gv) return gv.error();
   return ops::add(y.value(), gv.value(), s);
 }

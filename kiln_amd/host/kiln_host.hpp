@@ -174,8 +174,8 @@ Result<Array> take(const Array& a, const Array& indices, int axis, const Stream&
 // Embedding::lookup's take x3 + dequantize in one pass (nn.rs:159-176).
 Result<Array> quantized_embedding(const Array& ids, const Array& w, const Array& scales,
                                   const Array& biases, int group_size, int bits, const Stream& s);
-// a + b with b broadcast over a's leading dims (b.shape == a.shape[-b.ndim:]);
-// the Linear bias add of nn.rs:98-100.
+// a + b with numpy broadcasting (mlx_add); the Linear bias add of
+// nn.rs:98-100 and SwitchLinear's expert bias (moe.rs:166-172).
 Result<Array> add(const Array& a, const Array& b, const Stream& s);
 // Linear::forward's quantized matmul (transpose=true) and optional bias in
 // one launch (kh_linear): the product in its own dtype, then + bias.

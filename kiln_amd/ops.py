@@ -282,10 +282,11 @@ def take(a: torch.Tensor, indices: torch.Tensor, axis: int = 0, *,
 
 def add(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None,
         stream=None) -> torch.Tensor:
-    """a + b with b broadcast over a's leading dims (Linear's bias add,
+    """a + b with numpy broadcasting (ops::add; Linear's bias add,
     crates/kiln-models/src/nn.rs:98-100)."""
     if out is None:
-        out = torch.empty_like(a, dtype=result_dtype(a.dtype, b.dtype))
+        out = torch.empty(torch.broadcast_shapes(a.shape, b.shape), dtype=result_dtype(a.dtype, b.dtype),
+                          device=a.device)
     _check(_lib.lib().kh_add(_desc(out, "res"), _desc(a, "a"), _desc(b, "b"),
                              _stream_handle(a, stream)))
     return out

@@ -350,14 +350,16 @@ def test_qmm_partial_blocks(oracle, bits, gs, K, M):
                                          (torch.bfloat16, torch.float32, torch.float32),
                                          (torch.float16, torch.bfloat16, torch.float16)])
 @pytest.mark.parametrize("shape,bshape", [((5, 96), (96,)), ((2, 3, 4101), (4101,)),
-                                          ((2, 3, 8), (3, 8)), ((0, 16), (16,))])
+                                          ((2, 3, 8), (3, 8)), ((0, 16), (16,)), ((4, 1, 8), (3, 8)),
+                                          ((2, 3, 5, 7), (2, 3, 1, 7)), ((1, 5), (3, 1)), ((6,), (2, 4, 6))])
 def test_add_broadcast_bit_exact(adt, bdt, odt, shape, bshape):
-    """kh_add: each sum formed in float32 and rounded once (RNE) to the output
-    dtype — the same as IEEE float32 addition followed by one cast."""
+    """kh_add: numpy broadcasting (mlx_add), each sum formed in float32 and
+    rounded once (RNE) to the output dtype — the same as IEEE float32
+    addition followed by one cast."""
     g = torch.Generator().manual_seed(7)
     a = torch.randn(shape, generator=g).to(adt).cuda()
     b = torch.randn(bshape, generator=g).to(bdt).cuda()
-    out = torch.empty(shape, dtype=odt, device="cuda")
+    out = torch.empty(torch.broadcast_shapes(shape, bshape), dtype=odt, device="cuda")
     ops.add(a, b, out=out)
     ref = (a.float() + b.float()).to(odt)
     assert torch.equal(out.view(-1).cpu().view(torch.int16 if odt != torch.float32 else torch.int32),
@@ -365,10 +367,10 @@ def test_add_broadcast_bit_exact(adt, bdt, odt, shape, bshape):
 
 
 @pytest.mark.gpu
-def test_add_rejects_non_suffix_broadcast():
+def test_add_rejects_incompatible_shapes():
     a = torch.zeros((4, 8), dtype=torch.float16, device="cuda")
-    with pytest.raises(ops.KilnError):
-        ops.add(a, torch.zeros((4,), dtype=torch.float16, device="cuda"))
+    with pytest.raises(ops.KilnError, match="cannot broadcast"):
+        ops.add(a, torch.zeros((4,), dtype=torch.float16, device="cuda"), out=torch.empty_like(a))
 
 
 # ----------------------------------------------------------------- fused neighbours (q/k/v, gate/up)

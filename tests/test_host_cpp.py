@@ -136,6 +136,46 @@ def test_missing_quantization_block_is_an_error(tmp_path):
 
 
 @pytest.mark.gpu
+def test_switch_linear_bias_broadcasts(oracle, tmp_path):
+    """SwitchLinear's expert bias is added as y + expand_dims(bias[indices], -2)
+    (moe.rs:166-172) with numpy broadcasting: x [2, 1, 4, K] against indices
+    [2, 3] gives y [2, 3, 4, N], and each pair's bias row is broadcast over
+    its 4 rows."""
+    from safetensors.numpy import save_file
+    E, N, K, gs = 4, 48, 256, 64
+    Ls = [make_linear_numpy(N, K, gs, "q4", seed=90 + e) for e in range(E)]
+    bias = (np.random.default_rng(91).standard_normal((E, N)) * 0.1).astype(np.float16)
+    pre = "model.layers.0.mlp"
+    t = {f"{pre}.switch_mlp.up_proj.weight": np.stack([L["w"] for L in Ls]),
+         f"{pre}.switch_mlp.up_proj.scales": np.stack([L["scales"] for L in Ls]).view(np.float16),
+         f"{pre}.switch_mlp.up_proj.biases": np.stack([L["biases"] for L in Ls]).view(np.float16),
+         f"{pre}.switch_mlp.up_proj.bias": bias}
+    d = tmp_path / "bc"
+    d.mkdir()
+    save_file(t, str(d / "model.safetensors"))
+    (d / "config.json").write_text(json.dumps({"model_type": "olmoe",
+                                               "quantization": {"group_size": gs, "bits": 4}}))
+    ids = np.array([[0, 3, 1], [2, 2, 0]], dtype=np.uint32)
+    x = make_x_numpy(8, K, seed=92, xdt="f16").reshape(2, 1, 4, K)
+    (tmp_path / "x.bin").write_bytes(x.tobytes())
+    (tmp_path / "ids.bin").write_bytes(ids.tobytes())
+    rc, out, err = _job(tmp_path, model_dir=str(d), op="switch", prefix=pre, proj="up_proj", experts=E,
+                        input=str(tmp_path / "x.bin"), input_shape=[2, 1, 4, K], input_dtype="float16",
+                        ids=str(tmp_path / "ids.bin"), ids_shape=[2, 3], sorted=False,
+                        output=str(tmp_path / "y.bin"))
+    assert rc == 0 and out["ok"], (out, err)
+    assert out["shape"] == [2, 3, 4, N] and out["dtype"] == "float16"
+    y = np.frombuffer((tmp_path / "y.bin").read_bytes(), dtype=np.float16).astype(np.float64).reshape(2, 3, 4, N)
+    for i in range(2):
+        for j in range(3):
+            e = int(ids[i, j])
+            r16 = oracle.quantized_matmul(x[i, 0], "f16", Ls[e]["w"], Ls[e]["scales"], Ls[e]["biases"], "f16",
+                                          gs, 4, True, "f16")
+            ref = (oracle.to_f32(r16, "f16") + bias[e].astype(np.float32)).astype(np.float16).astype(np.float64)
+            assert np.max(np.abs(y[i, j] - ref)) <= 2e-2 * np.max(np.abs(ref)), (i, j)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("form", ["per_expert", "stacked"])
 @pytest.mark.parametrize("P", [6, 80])
 def test_switch_linear_from_checkpoint(oracle, tmp_path, form, P):
