@@ -55,8 +55,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--m", type=int, default=None, help="batch rows of --profile decode (default 1)")
-    ap.add_argument("--profile", choices=["decode", "decode8", "prefill", "traffic", "moe"], default=None,
+    ap.add_argument("--m", type=int, default=None, help="batch rows of --profile decode|qwen|head")
+    ap.add_argument("--gs", type=int, default=None, help="group size of --profile qwen (32 or 128)")
+    ap.add_argument("--profile", choices=["decode", "decode8", "prefill", "traffic", "moe", "qwen", "head",
+                                          "embed"], default=None,
                     help="run one workload for a profiler and exit (no JSON line): the M=1 decode "
                          "step, the M=2048 Llama-3-8B layer, or a copy of known size followed by "
                          "gate-shape GEMV launches (counter calibration)")
@@ -126,6 +128,10 @@ def main():
             for name, _, _ in shapes:
                 per[name](c)
         return step, per
+
+    if args.profile in ("qwen", "head", "embed"):
+        profile_other(args.profile, torch, ops, layer_copies, layer_fns, dev, args.m or 1, args.gs or 32)
+        return
 
     # ---------------- headline: Llama-3-8B decode step at M = 1
     gs, bits = 64, 4
@@ -278,6 +284,39 @@ def profile_run(kind, torch, ops, layers, shapes, layer_fns, dev, gs, bits, m=No
         for r in range(12):
             W = layers[r % len(layers)]["gate"]
             ops.quantized_matmul(x, W["w"], W["scales"], W["biases"], True, gs, bits, out=y)
+    torch.cuda.synchronize()
+
+
+def profile_other(kind, torch, ops, layer_copies, layer_fns, dev, m, gs):
+    """Workloads for rocprofv3 beyond the Llama-3-8B layer, eager launches over
+    weight copies beyond the MALL: the Qwen2.5-7B 8-bit layer (group size gs)
+    at M rows, the tied 128256x4096 gs128 LM head at M rows, and the
+    embedding gather of 4096 Zipf ids."""
+    from kiln_amd.workloads import LAYER_SHAPES
+    if kind == "qwen":
+        shapes = LAYER_SHAPES["qwen2.5-7b"]
+        layers = layer_copies(shapes, gs, "q8")
+        step, _ = layer_fns(layers, shapes, m, gs, 8)
+    else:
+        shapes = [("head", 128256, 4096)]
+        layers = layer_copies(shapes, 128, "emb")
+        if kind == "head":
+            step, _ = layer_fns(layers, shapes, m, 128, 4)
+        else:
+            import numpy as np
+            rng = np.random.default_rng(4000)
+            ids = []
+            while len(ids) < 4096:
+                z = rng.zipf(1.1, 8192) - 1
+                ids.extend(int(v) for v in z[z < 128256])
+            idt = torch.tensor(ids[:4096], dtype=torch.int32, device=dev)
+            eo = torch.empty((4096, 4096), dtype=torch.bfloat16, device=dev)
+
+            def step(c):
+                W = layers[c]["head"]
+                ops.quantized_embedding(idt, W["w"], W["scales"], W["biases"], 128, 4, out=eo)
+    for r in range(4 * len(layers)):
+        step(r % len(layers))
     torch.cuda.synchronize()
 
 

@@ -65,8 +65,24 @@ def build(verbose: bool = False, out: str = LIB, extra=(), build_dir: str = BUIL
     os.replace(tmp, out)
     if verbose:
         print(f"built {out}")
-    if out == LIB and os.path.exists(RUNNER_SRC):
-        build_runner(verbose)
+    if out == LIB:
+        if os.path.exists(RUNNER_SRC):
+            build_runner(verbose)
+        build_probes(verbose)
+    return out
+
+
+def build_probes(verbose: bool = False) -> str:
+    """The hardware-ceiling probes (kiln_amd/probes), a library of their own."""
+    src = os.path.join(HERE, "probes", "kh_probes.hip")
+    out = os.path.join(HERE, "probes", "libkh_probes.so")
+    cmd = [HIPCC, *CFLAGS, "-shared", src, "-o", out + ".tmp"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"building the probes failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(out + ".tmp", out)
+    if verbose:
+        print(f"built {out}")
     return out
 
 

@@ -1,0 +1,91 @@
+// kh_probes.hip — hardware ceilings the kernels of libkiln_hip are judged
+// against, measured on the same part (not part of the product path):
+//
+//   kp_empty        an empty kernel: the fixed cost of one launch (in a graph)
+//   kp_stream_read  a plain one-pass read of a buffer, 16 bytes per lane,
+//                   every byte once, fully coalesced: the attainable HBM read
+//                   rate at a given size (the decode GEMV's roofline in
+//                   practice)
+//   kp_mfma         independent v_mfma_f32_16x16x32_f16 chains per wave: the
+//                   dense fp16 matrix-core rate the part sustains
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__global__ void kp_empty_kernel(uint32_t* out) {
+  if (threadIdx.x == 0x7fffffff) out[0] = 1u;
+}
+
+// L loads in flight per lane; thread t reads chunks t + i*T (T threads).
+template <int L>
+__global__ __launch_bounds__(256) void kp_stream_read_kernel(const u32x4* __restrict__ w, int64_t n16,
+                                                             uint32_t* out) {
+  const int64_t T = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  u32x4 v[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    const int64_t j = t + i * T;
+    v[i] = __builtin_nontemporal_load(w + (j < n16 ? j : n16 - 1));
+  }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < L; ++i) acc ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+  if (acc == 0x9e3779b9u) out[0] = acc;  // keeps the loads; practically never stores
+}
+
+template <int ACC>
+__global__ __launch_bounds__(256) void kp_mfma_kernel(float* out, int iters) {
+  f32x4 acc[ACC];
+#pragma unroll
+  for (int i = 0; i < ACC; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (_Float16)(threadIdx.x * 0.001f + i);
+    b[i] = (_Float16)(i * 0.5f);
+  }
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < ACC; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[i], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < ACC; ++i) s += acc[i][0] + acc[i][1] + acc[i][2] + acc[i][3];
+  out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kp_empty(void* out, void* stream) {
+  hipLaunchKernelGGL(kp_empty_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, (uint32_t*)out);
+  return (int)hipGetLastError();
+}
+
+// One pass over `bytes` bytes (a multiple of 16) with 256-thread blocks and
+// 4 loads in flight per lane.
+int kp_stream_read(const void* w, int64_t bytes, void* out, void* stream) {
+  constexpr int L = 4;
+  const int64_t n16 = bytes / 16;
+  const int64_t blocks = (n16 + 256 * L - 1) / (256 * L);
+  if (n16 <= 0 || blocks > 0x7fffffff) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL((kp_stream_read_kernel<L>), dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const u32x4*)w, n16, (uint32_t*)out);
+  return (int)hipGetLastError();
+}
+
+// `wgs` workgroups of 4 waves, each wave `iters` x 32 independent MFMAs;
+// out holds wgs*256 floats. Flops: 2*16*16*32 * 32 * iters * 4 * wgs.
+int kp_mfma(void* out, int wgs, int iters, void* stream) {
+  hipLaunchKernelGGL((kp_mfma_kernel<32>), dim3(wgs), dim3(256), 0, (hipStream_t)stream, (float*)out, iters);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"
