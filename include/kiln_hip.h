@@ -113,11 +113,13 @@ typedef enum kh_status {
  * x: bfloat16 | float16 | float32; scales/biases: bfloat16 | float16 | float32
  * (same dtype for both); res: bfloat16 | float16 | float32. Products are
  * accumulated in float32 and rounded once (round-to-nearest-even) to res.
- * With bf16/f16 x and bf16/f16 scales, transpose=true and M <= 16 every
- * dequantised weight is used exactly; for M > 16 each weight is rounded once
- * to float16 (relative error <= 2^-11) before the float32-accumulating MFMA,
- * and x is scaled per row by an exact power of two into float16 range. Other
- * combinations run an exact float32 kernel.
+ * With bf16/f16 x and bf16/f16 scales and transpose=true, the decode kernels
+ * (M <= 16, and M <= 32 on shapes the small-batch kernel takes) use every
+ * dequantised weight exactly; the GEMM path (larger M; kh_quantized_matmul_plan
+ * names the kernel of a call) rounds each weight once to float16 (relative
+ * error <= 2^-11) before the float32-accumulating MFMA, with x scaled per row
+ * by an exact power of two into float16 range. Other combinations run an exact
+ * float32 kernel.
  * bits in {4, 8}; group_size in {32, 64, 128}; K % group_size == 0. */
 int kh_quantized_matmul(kh_array* res, const kh_array* x, const kh_array* w,
                         const kh_array* scales, const kh_array* biases,

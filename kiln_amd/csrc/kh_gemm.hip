@@ -55,24 +55,6 @@ __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// Pairs of codes as float16 (1024 + q) in both halves (exact for q < 1024),
-// in the pair order of permute_x: 4-bit word -> (c0,c4)(c1,c5)(c2,c6)(c3,c7);
-// 8-bit word pair -> (c0,c2)(c1,c3)(c4,c6)(c5,c7).
-template <int BITS>
-__device__ __forceinline__ void pairs_1024(uint32_t q0, uint32_t q1, uint32_t mag, uint32_t* r) {
-  if constexpr (BITS == 4) {
-    r[0] = (q0 & 0x000f000fu) | mag;
-    r[1] = ((q0 >> 4) & 0x000f000fu) | mag;
-    r[2] = ((q0 >> 8) & 0x000f000fu) | mag;
-    r[3] = ((q0 >> 12) & 0x000f000fu) | mag;
-  } else {
-    r[0] = (q0 & 0x00ff00ffu) | mag;
-    r[1] = ((q0 >> 8) & 0x00ff00ffu) | mag;
-    r[2] = (q1 & 0x00ff00ffu) | mag;
-    r[3] = ((q1 >> 8) & 0x00ff00ffu) | mag;
-  }
-}
-
 // 16-bit scale/bias halves -> (v, v) float16 pair. bf16 values are converted
 // through float32 to float16 (round to nearest even); scales and biases of
 // the supported formats are far inside float16's normal range.
@@ -84,15 +66,6 @@ __device__ __forceinline__ h2 half_pair(uint32_t h) {
     const _Float16 v = (_Float16)bf16_bits_to_f32(h);
     return h2{v, v};
   }
-}
-
-// Offset (codes) of the 8-code block lane group lg contributes to MFMA step j
-// of a stage: 4-bit lanes hold 32 consecutive codes (16 bytes), step j takes
-// word j; 8-bit lanes hold two 16-code runs 64 apart, step j takes words
-// 2(j%2), 2(j%2)+1 of run j/2.
-template <int BITS>
-__device__ __forceinline__ int step_off(int j, int lg) {
-  return BITS == 4 ? lg * 32 + 8 * j : (j >> 1) * 64 + lg * 16 + (j & 1) * 8;
 }
 
 // Stages kept in flight (measured on the Llama-3-8B shapes): 4 for the
