@@ -36,6 +36,13 @@ bool skinny_supported(int64_t M, int64_t N, int64_t K, int bits, int gs);
 // times the waves that split K (the largest divisor of K/128 up to 8).
 int64_t skinny_waves(int64_t N, int64_t K);
 hipError_t launch_skinny(const QmvArgs& a);
+// Up to 4 parts on one x (each skinny_supported, same M, K, bits, group size
+// and x/scales dtypes), one launch; each part's result equals launch_skinny's.
+hipError_t launch_skinny_multi(const QmvArgs* a, int n);
+// act(gate) * up (ACT_SILU / ACT_GELU_APPROX) in one launch, each output
+// summed as launch_skinny sums it; gate and up of equal shapes.
+bool skinny_pairable(const QmvArgs& gate);
+hipError_t launch_skinny_gate_up(const QmvArgs& gate, const QmvArgs& up, int act);
 
 // Largest M served by the decode kernel; larger M takes the prefill GEMM.
 constexpr int kDecodeMaxM = 16;

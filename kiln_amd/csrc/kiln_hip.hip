@@ -566,21 +566,33 @@ int multi(const char* op, int n, kh_array* const* res, const kh_array* x, const 
     }
     return KH_OK;
   }
-  bool fused = n <= 4;
-  for (int i = 0; i < n && fused; ++i)
-    fused = fast_path(a[i], transpose) && gemv_path(a[i]) && !skinny_path(a[i]) && a[i].sdt == a[0].sdt &&
-            a[i].odt == a[0].odt;
-  if (fused) {
-    const hipError_t e = kh::launch_gemv_multi(a.data(), n);
-    return e == hipSuccess ? KH_OK : hip_fail(op, e);
-  }
-  bool shared = true;  // every part on the prefill GEMM: convert x once
-  for (int i = 0; i < n && shared; ++i) shared = gemm_path(a[i], transpose);
-  if (shared) return run_gemm_parts(op, a.data(), n);
+  // Parts taking the same kernel class share launches: the decode GEMV's
+  // parts one multi-part launch, the small-batch MFMA kernel's parts one
+  // launch, the prefill GEMM's parts one activation conversion. Every part's
+  // result is what its own call gives.
+  std::vector<kh::QmvArgs> gv, sk, gm, rest;
   for (int i = 0; i < n; ++i) {
-    const int rc = run_qmm(op, a[i], transpose);
-    if (rc) return rc;
+    const kh::QmvArgs& p = a[i];
+    if (!fast_path(p, transpose) || n > 4)
+      rest.push_back(p);
+    else if (skinny_path(p) && p.sdt == a[0].sdt)
+      sk.push_back(p);
+    else if (gemv_path(p) && p.sdt == a[0].sdt && p.odt == a[0].odt)
+      gv.push_back(p);
+    else if (gemm_path(p, transpose))
+      gm.push_back(p);
+    else
+      rest.push_back(p);
   }
+  hipError_t e = hipSuccess;
+  if (!gv.empty()) e = gv.size() == 1 ? kh::launch_gemv(gv[0]) : kh::launch_gemv_multi(gv.data(), (int)gv.size());
+  if (e == hipSuccess && !sk.empty())
+    e = sk.size() == 1 ? kh::launch_skinny(sk[0]) : kh::launch_skinny_multi(sk.data(), (int)sk.size());
+  if (e != hipSuccess) return hip_fail(op, e);
+  if (!gm.empty())
+    if (int rc = run_gemm_parts(op, gm.data(), (int)gm.size())) return rc;
+  for (const kh::QmvArgs& p : rest)
+    if (int rc = run_qmm(op, p, transpose)) return rc;
   return KH_OK;
 }
 
@@ -643,6 +655,10 @@ int gate_up(const char* op, kh_array* res, const kh_array* x, const kh_array* w_
   if ((rc = check_device(op))) return rc;
   if (fast_path(g, true) && fast_path(u, true) && gemv_path(g) && !skinny_path(g) && g.sdt == u.sdt) {
     const hipError_t e = kh::launch_gemv_gate_up(g, u, activation);
+    return e == hipSuccess ? KH_OK : hip_fail(op, e);
+  }
+  if (fast_path(g, true) && fast_path(u, true) && skinny_path(g) && g.sdt == u.sdt && kh::skinny_pairable(g)) {
+    const hipError_t e = kh::launch_skinny_gate_up(g, u, activation);
     return e == hipSuccess ? KH_OK : hip_fail(op, e);
   }
   // Composite: gate and up into intermediates of the result dtype (workspace

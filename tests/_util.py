@@ -48,43 +48,27 @@ def gemv_max_m(K: int, bits: int) -> int:
     return 8 if I == 1 else 2 if I == 2 else 1 if I <= 4 else 0
 
 
-def skinny_fits(M: int, N: int, K: int, bits: int = 4) -> bool:
-    """The skinny MFMA kernel's range rule (kh_skinny.hip, skinny_path in
-    kiln_hip.hip): K % 128 == 0, 5 <= M <= 32; not where its launch has
-    fewer than 1024 waves (ceil(N/16) * W, W = the largest divisor of K/128
-    up to 8) and the decode GEMV takes M; above 16 rows only where those
-    waves fit one round."""
-    if K % 128 or not 5 <= M <= 32:
-        return False
-    np_ = K // 128
-    W = max(w for w in range(1, 9) if np_ % w == 0)
-    waves = -(-N // 16) * W
-    if M <= gemv_max_m(K, bits) and waves < 1024:
-        return False
-    if M <= 16:
-        return True
-    return waves <= 3 * 4 * 256
-
-
-def decode_regime(M: int, K: int, bits: int, N: int):
+def decode_regime(M: int, K: int, bits: int, N: int, gs: int = 64):
     """Which kernel (and tiling class) kh_quantized_matmul uses for a
-    transpose=true call with bf16/f16 x and 16-bit scales: rows of the result
-    are bitwise identical for every M of one regime (kiln_hip.hip, run_qmm)."""
-    if skinny_fits(M, N, K, bits):
-        return ("skinny",)
-    if M <= gemv_max_m(K, bits):
-        return ("gemv",)
-    if K % 128 == 0:
-        mt = 1
-        while mt < 8 and 16 * mt < M:
-            mt *= 2
+    transpose=true call with bf16 x and f16 scales, as the library's own plan
+    names it (kh_quantized_matmul_plan, no GPU needed): rows of the result
+    are bitwise identical for every M of one regime (kiln_hip.hip, run_qmm).
+    The GEMM's class is its m-tile, and for 128-row tiles the number of
+    row tiles (the split-K plan depends on them)."""
+    from kiln_amd import ops
+    plan = ops.quantized_matmul_plan(M, N, K, gs, bits)
+    kind = plan.split()[0]
+    if kind == "gemm":
+        mt = int(dict(kv.split("=") for kv in plan.split()[1:])["mt"])
         return ("gemm", mt, -(-M // 128) if mt == 8 else 1)
-    return ("qmv",) if M <= 16 else ("qmm", -(-M // 256))
+    if kind == "qmm":
+        return ("qmm", -(-M // 256))
+    return (kind,)
 
 
-def exact_weights(M: int, K: int, bits: int, N: int) -> bool:
+def exact_weights(M: int, K: int, bits: int, N: int, gs: int = 64) -> bool:
     """True where every dequantised weight enters the products unrounded
     (the decode GEMV, the skinny MFMA kernel and qmv); the GEMM kernels round
     each weight once to fp16."""
-    r = decode_regime(M, K, bits, N)[0]
+    r = decode_regime(M, K, bits, N, gs)[0]
     return r in ("gemv", "skinny", "qmv")

@@ -101,12 +101,13 @@ def _gate_up_case(M, N, K, seed, bias):
 
 
 @pytest.mark.parametrize("act", [_lib.ACT_SILU, _lib.ACT_GELU_APPROX])
-@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("M", [1, 4, 12, 24])
 def test_mlp_gate_up_fused_equals_composite(act, M):
-    """On the fused decode launch (gate and up with the same scale dtype) and
-    on the composite path (up's scales in the other 16-bit dtype, same
-    values: two matmul launches, then the activation kernel) the result is
-    bit-identical."""
+    """On the fused launch (gate and up with the same scale dtype: the decode
+    GEMV at M = 1, 4, the small-batch MFMA kernel in paired mode at M = 12,
+    24) and on the composite path (up's scales in the other 16-bit dtype,
+    same values: two matmul launches, then the activation kernel) the result
+    is bit-identical."""
     print(f"case mlp_gate_up act={act} M={M}", flush=True)
     N, K = 272, 2048
     xd, gate, up, up_bf, _ = _gate_up_case(M, N, K, 70 + M, False)
@@ -117,7 +118,7 @@ def test_mlp_gate_up_fused_equals_composite(act, M):
 
 
 @pytest.mark.parametrize("act", [_lib.ACT_SILU, _lib.ACT_GELU_APPROX])
-@pytest.mark.parametrize("M", [1, 4, 40])
+@pytest.mark.parametrize("M", [1, 4, 12, 40])
 def test_mlp_gate_up_biases(oracle, act, M):
     """With gate and up biases (mlp_bias models): the activation of the
     device's own kh_linear results, to one unit in the last place (host

@@ -50,14 +50,14 @@ def _run(L, x, gs, bits, xdt, sdt, odt, transpose=True):
 EXACT_REL, F16W_REL = 3e-5, 2.0 ** -11 + 3e-5
 
 
-def rel_for(M, K, bits, transpose=True, N=1):
-    return EXACT_REL if (not transpose or exact_weights(M, K, bits, N)) else F16W_REL
+def rel_for(M, K, bits, transpose=True, N=1, gs=64):
+    return EXACT_REL if (not transpose or exact_weights(M, K, bits, N, gs)) else F16W_REL
 
 
 def _check_f32(oracle, L, x, gs, bits, xdt, sdt, y, transpose=True, rel=None):
     if rel is None:
         N = L["w"].shape[0] if transpose else L["w"].shape[1] * (32 // bits)
-        rel = rel_for(x.reshape(-1, x.shape[-1]).shape[0], x.shape[-1], bits, transpose, N)
+        rel = rel_for(x.reshape(-1, x.shape[-1]).shape[0], x.shape[-1], bits, transpose, N, gs)
     ref = oracle.quantized_matmul_f32(x, xdt, L["w"], L["scales"], L["biases"], sdt, gs, bits, transpose)
     W = oracle.to_f32(oracle.dequantize(L["w"], L["scales"], L["biases"], sdt, gs, bits, "f32"), "f32")
     mag = np.abs(oracle.to_f32(x, xdt)).astype(np.float64) @ np.abs(W.T if transpose else W).astype(np.float64)
@@ -153,7 +153,7 @@ def test_rows_are_m_invariant(bits, gs, K):
     L, x = _case(200, N, K, gs, bits, seed=21)
     groups = {}
     for M in (1, 2, 3, 4, 5, 6, 15, 16, 17, 20, 31, 32, 33, 64, 65, 100, 128, 129, 200):
-        groups.setdefault(decode_regime(M, K, bits, N), []).append(M)
+        groups.setdefault(decode_regime(M, K, bits, N, gs), []).append(M)
     for regime, Ms in groups.items():
         big = _run(L, x[:max(Ms)], gs, bits, "bf16", "f16", "bf16")
         for M in Ms[:-1]:
@@ -375,13 +375,16 @@ def test_add_rejects_incompatible_shapes():
 
 # ----------------------------------------------------------------- fused neighbours (q/k/v, gate/up)
 
-@pytest.mark.parametrize("M", [1, 3, 8, 9, 40, 300])
+@pytest.mark.parametrize("M", [1, 3, 6, 8, 9, 12, 24, 40, 300])
 @pytest.mark.parametrize("bits,gs", [(4, 64), (8, 128)])
 def test_multi_equals_separate_calls(M, bits, gs):
     """kh_quantized_matmul_multi (the q/k/v triple on one x, nn.rs:724-726)
-    returns, part by part, the bits of separate kh_quantized_matmul calls."""
+    returns, part by part, the bits of separate kh_quantized_matmul calls:
+    one decode GEMV launch (M <= 8), one small-batch MFMA launch (M = 9..32),
+    and at M = 6 the wide part on the MFMA kernel with the narrow parts'
+    GEMV launch beside it; the prefill GEMM from M = 40."""
     K = 1024
-    shapes = [(256, K), (64, K), (64, K)]
+    shapes = [(2048 if M == 6 else 256, K), (64, K), (64, K)]
     parts, host_parts = [], []
     for i, (N, _) in enumerate(shapes):
         L = make_linear_numpy(N, K, gs, "q4" if bits == 4 else "q8", seed=40 + i)
@@ -389,6 +392,9 @@ def test_multi_equals_separate_calls(M, bits, gs):
         parts.append((dev(L["w"]), dev(L["scales"], "f16"), dev(L["biases"], "f16")))
     x = dev(make_x_numpy(M, K, seed=44), "bf16")
     outs = ops.quantized_matmul_multi(x, parts, True, gs, bits, out_dtype="bf16")
+    if M == 6:
+        plans = [ops.quantized_matmul_plan(M, N, K, gs, bits, torch.bfloat16, torch.float16) for N, _ in shapes]
+        assert plans[0] == "skinny" and plans[1] == plans[2] == "gemv", plans
     for (w, s, b), o in zip(parts, outs):
         ref = ops.quantized_matmul(x, w, s, b, True, gs, bits, out_dtype="bf16")
         assert torch.equal(o.view(torch.int16), ref.view(torch.int16))
@@ -744,7 +750,7 @@ def test_skinny_kernel_exact(oracle, bits, gs, xdt):
     cases += [(N, K, M) for N, K in ((16390, 128), (2360, 896), (2050, 4096)) for M in (5, 8)]
     for N, K, M in cases:
         print(f"case skinny bits={bits} gs={gs} xdt={xdt} N={N} K={K} M={M}", flush=True)
-        assert decode_regime(M, K, bits, N)[0] == "skinny"
+        assert decode_regime(M, K, bits, N, gs)[0] == "skinny"
         L, x = _case(M, N, K, gs, bits, xdt=xdt, seed=M + N + K + bits)
         y = _run(L, x, gs, bits, xdt, "f16", "f32")
         _check_f32(oracle, L, x, gs, bits, xdt, "f16", y, rel=EXACT_REL)
