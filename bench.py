@@ -320,18 +320,18 @@ def profile_other(kind, torch, ops, layer_copies, layer_fns, dev, m, gs):
     torch.cuda.synchronize()
 
 
-def fused_step(torch, ops, layers, shapes, graph_us, dev, g, gs, bits, copies, reps):
-    """The same M = 1 layer through the fused entry points (SURVEY next row:
-    fused neighbours): q|k|v in one kh_quantized_matmul_multi launch, o,
-    silu(gate)*up in one kh_quantized_gate_up launch, down. Algorithmic bytes
-    count x once per launch and the one activation output."""
+def fused_step(torch, ops, layers, shapes, graph_us, dev, g, gs, bits, copies, reps, M=1):
+    """The same layer (M rows) through the fused entry points (SURVEY next
+    row: fused neighbours): q|k|v in one kh_quantized_matmul_multi call, o,
+    silu(gate)*up in one kh_quantized_gate_up call, down. Algorithmic bytes
+    count x once per call and the one activation output."""
     Ns = {n: (N, K) for n, N, K in shapes}
-    x = torch.randn((1, Ns["q"][1]), generator=g, device=dev).bfloat16()
-    xd = torch.randn((1, Ns["down"][1]), generator=g, device=dev).bfloat16()
-    qkv = [torch.empty((1, Ns[n][0]), dtype=torch.bfloat16, device=dev) for n in ("q", "k", "v")]
-    o = torch.empty((1, Ns["o"][0]), dtype=torch.bfloat16, device=dev)
-    act = torch.empty((1, Ns["gate"][0]), dtype=torch.bfloat16, device=dev)
-    y = torch.empty((1, Ns["down"][0]), dtype=torch.bfloat16, device=dev)
+    x = torch.randn((M, Ns["q"][1]), generator=g, device=dev).bfloat16()
+    xd = torch.randn((M, Ns["down"][1]), generator=g, device=dev).bfloat16()
+    qkv = [torch.empty((M, Ns[n][0]), dtype=torch.bfloat16, device=dev) for n in ("q", "k", "v")]
+    o = torch.empty((M, Ns["o"][0]), dtype=torch.bfloat16, device=dev)
+    act = torch.empty((M, Ns["gate"][0]), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((M, Ns["down"][0]), dtype=torch.bfloat16, device=dev)
 
     def step(c):
         L = layers[c]
@@ -343,9 +343,10 @@ def fused_step(torch, ops, layers, shapes, graph_us, dev, g, gs, bits, copies, r
 
     us = graph_us(step, copies, reps)
     wb = lambda n: Ns[n][0] * Ns[n][1] * bits // 8 + 2 * Ns[n][0] * (Ns[n][1] // gs) * 2
-    nbytes = (sum(wb(n) for n in ("q", "k", "v", "o", "gate", "up", "down")) + 2 * 2 * Ns["q"][1]
-              + 2 * Ns["down"][1] + 2 * (sum(Ns[n][0] for n in ("q", "k", "v", "o", "down")) + Ns["gate"][0]))
-    return {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "launches": 4,
+    nbytes = (sum(wb(n) for n in ("q", "k", "v", "o", "gate", "up", "down")) + 3 * 2 * M * Ns["q"][1]
+              + 2 * M * Ns["down"][1]
+              + 2 * M * (sum(Ns[n][0] for n in ("q", "k", "v", "o", "down")) + Ns["gate"][0]))
+    return {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "calls": 4,
             "bytes": nbytes}
 
 
@@ -376,6 +377,10 @@ def run_sweep(torch, ops, l8_layers, l8_shapes, graph_us, layer_fns, layer_copie
     out["llama-3-8b"] = {"decode": measure(l8_layers, l8_shapes, (1, 8, 32, 64), 64, 4, lambda M: 20),
                          "prefill": measure(l8_layers[:2], l8_shapes, (512, 2048, 4096), 64, 4,
                                             lambda M: 3)}
+    out["llama-3-8b"]["decode_fused"] = {
+        str(M): fused_step(torch, ops, l8_layers, l8_shapes, graph_us, dev, g, 64, 4, len(l8_layers), 20, M)
+        for M in (1, 8, 32, 64)}
+    print(f"# sweep fused decode: {out['llama-3-8b']['decode_fused']}", file=sys.stderr, flush=True)
     pf = out["llama-3-8b"]["prefill"]["2048"]
     pf["frac_of_bf16_peak"] = round(pf["tflops"] / BF16_PEAK_TFLOPS, 4)
 

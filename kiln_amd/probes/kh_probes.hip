@@ -8,6 +8,8 @@
 //                   practice)
 //   kp_mfma         independent v_mfma_f32_16x16x32_f16 chains per wave: the
 //                   dense fp16 matrix-core rate the part sustains
+//   kp_mfma32       the same with v_mfma_f32_32x32x16_f16 (twice the flops
+//                   per instruction, half the operand bytes per flop)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -60,6 +62,32 @@ __global__ __launch_bounds__(256) void kp_mfma_kernel(float* out, int iters) {
   out[blockIdx.x * 256 + threadIdx.x] = s;
 }
 
+template <int ACC>
+__global__ __launch_bounds__(256) void kp_mfma32_kernel(float* out, int iters) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  f32x16 acc[ACC];
+#pragma unroll
+  for (int i = 0; i < ACC; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
+  f16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (_Float16)(threadIdx.x * 0.001f + i);
+    b[i] = (_Float16)(i * 0.5f);
+  }
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < ACC; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < ACC; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += acc[i][e];
+  out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
 }  // namespace
 
 extern "C" {
@@ -83,6 +111,12 @@ int kp_stream_read(const void* w, int64_t bytes, void* out, void* stream) {
 
 // `wgs` workgroups of 4 waves, each wave `iters` x 32 independent MFMAs;
 // out holds wgs*256 floats. Flops: 2*16*16*32 * 32 * iters * 4 * wgs.
+// 8 independent 32x32x16 chains per wave: 2 * 32*32*16 * 8 flops per wave and iteration.
+int kp_mfma32(void* out, int wgs, int iters, void* stream) {
+  hipLaunchKernelGGL((kp_mfma32_kernel<8>), dim3(wgs), dim3(256), 0, (hipStream_t)stream, (float*)out, iters);
+  return (int)hipGetLastError();
+}
+
 int kp_mfma(void* out, int wgs, int iters, void* stream) {
   hipLaunchKernelGGL((kp_mfma_kernel<32>), dim3(wgs), dim3(256), 0, (hipStream_t)stream, (float*)out, iters);
   return (int)hipGetLastError();

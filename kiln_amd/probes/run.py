@@ -8,8 +8,9 @@
   launches (cfg0 9.4 MB, a Llama-3-8B gate 33 MB, twice that, the 279 MB LM
   head, 600 MB), each replayed over enough distinct buffers (> 600 MB) that
   the 256 MB MALL cannot serve them: us per launch and GB/s;
-- mfma: independent v_mfma_f32_16x16x32_f16 chains at one and two waves per
-  SIMD on all 256 CUs: TFLOP/s against the 2.5 PFLOP/s dense fp16 peak.
+- mfma: independent v_mfma_f32_16x16x32_f16 chains (and 32x32x16 chains) at
+  one and two waves per SIMD on all 256 CUs: TFLOP/s against the 2.5 PFLOP/s
+  dense fp16 peak.
 """
 from __future__ import annotations
 
@@ -67,22 +68,26 @@ def main():
         del bufs
     res["stream_read"] = reads
 
-    mf = {}
-    iters = 20000
-    for wgs in (256, 512):
-        L.kp_mfma(ctypes.c_void_p(out.data_ptr()), wgs, 100, st())
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        assert L.kp_mfma(ctypes.c_void_p(out.data_ptr()), wgs, iters, st()) == 0
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1)
-        flops = 2.0 * 16 * 16 * 32 * 32 * iters * 4 * wgs
-        tf = flops / ms / 1e9
-        mf[f"{wgs // 256}_waves_per_simd"] = {"ms": round(ms, 3), "tflops": round(tf, 1),
-                                              "frac_of_2500": round(tf / 2500, 4)}
-    res["mfma_f16_16x16x32"] = mf
+    L.kp_mfma32.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+
+    def mfma_rate(fn, flops_per_wave_iter, iters=20000):
+        r = {}
+        for wgs in (256, 512):
+            fn(ctypes.c_void_p(out.data_ptr()), wgs, 100, st())
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            assert fn(ctypes.c_void_p(out.data_ptr()), wgs, iters, st()) == 0
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1)
+            tf = flops_per_wave_iter * iters * 4 * wgs / ms / 1e9
+            r[f"{wgs // 256}_waves_per_simd"] = {"ms": round(ms, 3), "tflops": round(tf, 1),
+                                                 "frac_of_2500": round(tf / 2500, 4)}
+        return r
+
+    res["mfma_f16_16x16x32"] = mfma_rate(L.kp_mfma, 2.0 * 16 * 16 * 32 * 32)      # 32 chains
+    res["mfma_f16_32x32x16"] = mfma_rate(L.kp_mfma32, 2.0 * 32 * 32 * 16 * 8)     # 8 chains
     print(json.dumps(res), flush=True)
 
 
