@@ -6,7 +6,7 @@
 //                   every byte once, fully coalesced: the attainable HBM read
 //                   rate at a given size (the decode GEMV's roofline in
 //                   practice)
-//   kp_mfma         independent v_mfma_f32_16x16x32_f16 chains per wave: the
+//   kp_mfma         8 independent v_mfma_f32_16x16x32_f16 chains per wave: the
 //                   dense fp16 matrix-core rate the part sustains
 //   kp_mfma32       the same with v_mfma_f32_32x32x16_f16 (twice the flops
 //                   per instruction, half the operand bytes per flop)
@@ -41,51 +41,50 @@ __global__ __launch_bounds__(256) void kp_stream_read_kernel(const u32x4* __rest
   if (acc == 0x9e3779b9u) out[0] = acc;  // keeps the loads; practically never stores
 }
 
-template <int ACC>
+// Independent accumulator chains, issued by inline asm on fixed registers:
+// written in C, the compiler rotates the accumulators of such a loop through
+// v_accvgpr_mov copies (four per MFMA), and the loop then measures the moves.
+// a, b: float16 1.0 / 0.5 (finite values; the rate does not depend on them).
 __global__ __launch_bounds__(256) void kp_mfma_kernel(float* out, int iters) {
-  f32x4 acc[ACC];
-#pragma unroll
-  for (int i = 0; i < ACC; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  f16x8 a, b;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a[i] = (_Float16)(threadIdx.x * 0.001f + i);
-    b[i] = (_Float16)(i * 0.5f);
-  }
+  f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0, c3 = c0, c4 = c0, c5 = c0, c6 = c0, c7 = c0;
+  const u32x4 a = {0x3c003c00u + (threadIdx.x & 1u), 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
+  const u32x4 b = {0x38003800u, 0x38003800u, 0x38003800u, 0x38003800u};
   for (int it = 0; it < iters; ++it) {
-#pragma unroll
-    for (int i = 0; i < ACC; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[i], 0, 0, 0);
+    asm volatile(
+        "v_mfma_f32_16x16x32_f16 %0, %8, %9, %0\n"
+        "v_mfma_f32_16x16x32_f16 %1, %8, %9, %1\n"
+        "v_mfma_f32_16x16x32_f16 %2, %8, %9, %2\n"
+        "v_mfma_f32_16x16x32_f16 %3, %8, %9, %3\n"
+        "v_mfma_f32_16x16x32_f16 %4, %8, %9, %4\n"
+        "v_mfma_f32_16x16x32_f16 %5, %8, %9, %5\n"
+        "v_mfma_f32_16x16x32_f16 %6, %8, %9, %6\n"
+        "v_mfma_f32_16x16x32_f16 %7, %8, %9, %7\n"
+        : "+a"(c0), "+a"(c1), "+a"(c2), "+a"(c3), "+a"(c4), "+a"(c5), "+a"(c6), "+a"(c7)
+        : "v"(a), "v"(b));
   }
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < ACC; ++i) s += acc[i][0] + acc[i][1] + acc[i][2] + acc[i][3];
-  out[blockIdx.x * 256 + threadIdx.x] = s;
+  const f32x4 s = c0 + c1 + c2 + c3 + c4 + c5 + c6 + c7;
+  out[blockIdx.x * 256 + threadIdx.x] = s[0] + s[1] + s[2] + s[3];
 }
 
-template <int ACC>
 __global__ __launch_bounds__(256) void kp_mfma32_kernel(float* out, int iters) {
   typedef float f32x16 __attribute__((ext_vector_type(16)));
-  f32x16 acc[ACC];
-#pragma unroll
-  for (int i = 0; i < ACC; ++i)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
-  f16x8 a, b;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a[i] = (_Float16)(threadIdx.x * 0.001f + i);
-    b[i] = (_Float16)(i * 0.5f);
-  }
+  f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  const u32x4 a = {0x3c003c00u + (threadIdx.x & 1u), 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
+  const u32x4 b = {0x38003800u, 0x38003800u, 0x38003800u, 0x38003800u};
   for (int it = 0; it < iters; ++it) {
-#pragma unroll
-    for (int i = 0; i < ACC; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
+    asm volatile(
+        "v_mfma_f32_32x32x16_f16 %0, %4, %5, %0\n"
+        "v_mfma_f32_32x32x16_f16 %1, %4, %5, %1\n"
+        "v_mfma_f32_32x32x16_f16 %2, %4, %5, %2\n"
+        "v_mfma_f32_32x32x16_f16 %3, %4, %5, %3\n"
+        : "+a"(c0), "+a"(c1), "+a"(c2), "+a"(c3)
+        : "v"(a), "v"(b));
   }
-  float s = 0.f;
+  const f32x16 s = c0 + c1 + c2 + c3;
+  float t = 0.f;
 #pragma unroll
-  for (int i = 0; i < ACC; ++i)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) s += acc[i][e];
-  out[blockIdx.x * 256 + threadIdx.x] = s;
+  for (int i = 0; i < 16; ++i) t += s[i];
+  out[blockIdx.x * 256 + threadIdx.x] = t;
 }
 
 }  // namespace
@@ -111,14 +110,14 @@ int kp_stream_read(const void* w, int64_t bytes, void* out, void* stream) {
 
 // `wgs` workgroups of 4 waves, each wave `iters` x 32 independent MFMAs;
 // out holds wgs*256 floats. Flops: 2*16*16*32 * 32 * iters * 4 * wgs.
-// 8 independent 32x32x16 chains per wave: 2 * 32*32*16 * 8 flops per wave and iteration.
+// 4 independent 32x32x16 chains per wave: 2 * 32*32*16 * 4 flops per wave and iteration.
 int kp_mfma32(void* out, int wgs, int iters, void* stream) {
-  hipLaunchKernelGGL((kp_mfma32_kernel<8>), dim3(wgs), dim3(256), 0, (hipStream_t)stream, (float*)out, iters);
+  hipLaunchKernelGGL(kp_mfma32_kernel, dim3(wgs), dim3(256), 0, (hipStream_t)stream, (float*)out, iters);
   return (int)hipGetLastError();
 }
 
 int kp_mfma(void* out, int wgs, int iters, void* stream) {
-  hipLaunchKernelGGL((kp_mfma_kernel<32>), dim3(wgs), dim3(256), 0, (hipStream_t)stream, (float*)out, iters);
+  hipLaunchKernelGGL(kp_mfma_kernel, dim3(wgs), dim3(256), 0, (hipStream_t)stream, (float*)out, iters);
   return (int)hipGetLastError();
 }
 

@@ -72,7 +72,7 @@ def main():
 
     def mfma_rate(fn, flops_per_wave_iter, iters=20000):
         r = {}
-        for wgs in (256, 512):
+        for wgs in (256, 512, 1024):
             fn(ctypes.c_void_p(out.data_ptr()), wgs, 100, st())
             torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -86,8 +86,8 @@ def main():
                                                  "frac_of_2500": round(tf / 2500, 4)}
         return r
 
-    res["mfma_f16_16x16x32"] = mfma_rate(L.kp_mfma, 2.0 * 16 * 16 * 32 * 32)      # 32 chains
-    res["mfma_f16_32x32x16"] = mfma_rate(L.kp_mfma32, 2.0 * 32 * 32 * 16 * 8)     # 8 chains
+    res["mfma_f16_16x16x32"] = mfma_rate(L.kp_mfma, 2.0 * 16 * 16 * 32 * 8)      # 8 chains
+    res["mfma_f16_32x32x16"] = mfma_rate(L.kp_mfma32, 2.0 * 32 * 32 * 16 * 4)     # 4 chains
     print(json.dumps(res), flush=True)
 
 
