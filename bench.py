@@ -55,9 +55,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--m", type=int, default=None, help="batch rows of --profile decode|qwen|head")
+    ap.add_argument("--m", type=int, default=None, help="batch rows of --profile decode|fused|qwen|head")
     ap.add_argument("--gs", type=int, default=None, help="group size of --profile qwen (32 or 128)")
-    ap.add_argument("--profile", choices=["decode", "decode8", "prefill", "traffic", "moe", "qwen", "head",
+    ap.add_argument("--profile", choices=["decode", "decode8", "fused", "prefill", "traffic", "moe", "qwen", "head",
                                           "embed"], default=None,
                     help="run one workload for a profiler and exit (no JSON line): the M=1 decode "
                          "step, the M=2048 Llama-3-8B layer, or a copy of known size followed by "
@@ -238,6 +238,13 @@ def profile_run(kind, torch, ops, layers, shapes, layer_fns, dev, gs, bits, m=No
         step, _ = layer_fns(layers, shapes, m or 1, gs, bits)
         for r in range(4 * len(layers)):
             step(r % len(layers))
+    elif kind == "fused":
+        # the layer through the fused entry points (q|k|v, gate_up) at M rows
+        g = torch.Generator(device=dev)
+        g.manual_seed(7)
+        step, _ = fused_fns(torch, ops, layers, shapes, dev, g, gs, bits, m or 1)
+        for r in range(4 * len(layers)):
+            step(r % len(layers))
     elif kind == "decode8":
         # small-batch decode: the 7 linears at M = 8 over the rotated copies
         step, _ = layer_fns(layers, shapes, 8, gs, bits)
@@ -320,11 +327,11 @@ def profile_other(kind, torch, ops, layer_copies, layer_fns, dev, m, gs):
     torch.cuda.synchronize()
 
 
-def fused_step(torch, ops, layers, shapes, graph_us, dev, g, gs, bits, copies, reps, M=1):
-    """The same layer (M rows) through the fused entry points (SURVEY next
-    row: fused neighbours): q|k|v in one kh_quantized_matmul_multi call, o,
-    silu(gate)*up in one kh_quantized_gate_up call, down. Algorithmic bytes
-    count x once per call and the one activation output."""
+def fused_fns(torch, ops, layers, shapes, dev, g, gs, bits, M=1):
+    """The layer (M rows) through the fused entry points: q|k|v in one
+    kh_quantized_matmul_multi call, o, silu(gate)*up in one
+    kh_quantized_gate_up call, down. Returns (step(copy index), algorithmic
+    bytes of one step: x counted once per call, the one activation output)."""
     Ns = {n: (N, K) for n, N, K in shapes}
     x = torch.randn((M, Ns["q"][1]), generator=g, device=dev).bfloat16()
     xd = torch.randn((M, Ns["down"][1]), generator=g, device=dev).bfloat16()
@@ -341,11 +348,17 @@ def fused_step(torch, ops, layers, shapes, graph_us, dev, g, gs, bits, copies, r
         ops.quantized_gate_up(x, W("gate"), W("up"), gs, bits, out=act)
         ops.quantized_matmul(xd, *W("down"), True, gs, bits, out=y)
 
-    us = graph_us(step, copies, reps)
     wb = lambda n: Ns[n][0] * Ns[n][1] * bits // 8 + 2 * Ns[n][0] * (Ns[n][1] // gs) * 2
     nbytes = (sum(wb(n) for n in ("q", "k", "v", "o", "gate", "up", "down")) + 3 * 2 * M * Ns["q"][1]
               + 2 * M * Ns["down"][1]
               + 2 * M * (sum(Ns[n][0] for n in ("q", "k", "v", "o", "down")) + Ns["gate"][0]))
+    return step, nbytes
+
+
+def fused_step(torch, ops, layers, shapes, graph_us, dev, g, gs, bits, copies, reps, M=1):
+    """Graph-replayed time of the fused layer of fused_fns (4 calls)."""
+    step, nbytes = fused_fns(torch, ops, layers, shapes, dev, g, gs, bits, M)
+    us = graph_us(step, copies, reps)
     return {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "calls": 4,
             "bytes": nbytes}
 

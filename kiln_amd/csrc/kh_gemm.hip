@@ -323,15 +323,25 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
       __builtin_amdgcn_s_barrier();
       const int pn = (p + P - 1) % P;  // slot and buffer of stage st + P - 1 (constant once unrolled)
       const int stn = min(st + P - 1, nst - 1);
+      // The waits count the ops issued after a stage's last activation load,
+      // so activation, scale and code loads leave in exactly this order (the
+      // scheduler would otherwise move code loads above the activation load
+      // of the same part, leaving that load outside the wait).
       auto issue = [&](int j) {  // part j of the spread issue
-        if (j == 0 && p == 0) load_scales(min(c + 1, nchunks - 1));
+        if (j == 0 && p == 0) {
+          load_scales(min(c + 1, nchunks - 1));
+          __builtin_amdgcn_sched_barrier(0);
+        }
         load_acts_part(pn, stn, j);
+        __builtin_amdgcn_sched_barrier(0);
         load_codes_part(q[pn], stn, j);
         __builtin_amdgcn_sched_barrier(0);
       };
       if constexpr (!SPREAD) {
         load_acts(pn, stn);
+        __builtin_amdgcn_sched_barrier(0);
         if (p == 0) load_scales(min(c + 1, nchunks - 1));
+        __builtin_amdgcn_sched_barrier(0);
         load_codes(q[pn], stn);
       }
       // The waits above rely on program order of the vector memory ops.
