@@ -9,21 +9,27 @@
 // Numerics: exact products, as the decode GEMV. Codes enter an MFMA as the
 // 16-bit values OFF + q built by OR-ing the code into the mantissa of OFF
 // (bf16 x: OFF = 128, f16 x: OFF = 1024; exact), against x in its own dtype,
-// accumulating in float32. Each MFMA step is restricted to one quantization
-// group by zeroing the A-operand lanes of the other groups, and a second MFMA
-// against ones gives the group sums X of x. Per group and piece:
+// accumulating in float32. MFMA step j of a 128-code piece covers the codes
+// j*32 .. j*32+31, which lie in one quantization group (group size >= 32),
+// and a second MFMA against ones gives the group sums X of x. Per group:
 //   acc += s * P + (b - OFF * s) * X,   P = sum x * (OFF + q).
 // 8-bit codes with bf16 x, where OFF + q is not exact beyond q = 127, enter
 // as two nibble operands: P = P_lo + 16 * P_hi with OFF_eff = 17 * 128.
 //
 // Work decomposition: a workgroup of W <= 8 waves owns 16 * NTW weight rows
-// and all M rows of x (one or two 16-row m-tiles);
-// the waves split K into 128-code pieces (wave w takes pieces w*ppw ..
-// (w+1)*ppw - 1). Within a piece, lane (n = l % 16, kb = l / 16) of a 16-row
-// tile loads the 32 codes kb*32 .. kb*32+31 of row n (16 or 32 bytes) and the
-// matching 32 values of x row l % 16; MFMA step j (0..3) takes the lane's
-// 8 codes 8j .. 8j+7. The loads of the next piece are in flight while a
-// piece computes. The W partial tiles are summed through LDS in wave order.
+// and all M rows of x (one or two 16-row m-tiles); the waves split K into
+// 128-code pieces, interleaved (wave w takes pieces w, w + W, ...), so at any
+// time a workgroup reads W consecutive pieces of each of its rows. Lane
+// (n = l % 16, kb = l / 16) of a 16-row tile loads the codes kb*32 ..
+// kb*32+31 of row n (16 or 32 bytes); a 4x4 word transpose across the lane
+// rows (permlane swaps) gives each lane its 8 codes of every step. x comes
+// as the matching 16-byte runs of x row l % 16 (zeros past M), straight
+// from memory. Every load is a buffer load whose offset is selected without
+// branches (past the row, the piece range or M it reads zeros), so the
+// compiler's waits cover exactly the piece computed while the next ones stay
+// in flight. The scales and biases of the workgroup's rows for all of K are
+// copied into LDS first, as contiguous 16-byte words. The W partial tiles
+// are summed through LDS in wave order.
 #include <algorithm>
 #include <type_traits>
 
@@ -37,6 +43,10 @@ namespace {
 constexpr int kSkMaxWaves = 8;
 constexpr int kSkMaxParts = 4;
 constexpr int kPiece = 128;  // codes per piece
+// Pieces a wave keeps in flight: one while it has at most kSkDepth1Max
+// pieces to do (measured best: more outstanding loads of this access
+// pattern only slowed the launch), two for longer runs of K.
+constexpr int kSkDepth1Max = 16;
 
 template <bool XBF16>
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
@@ -47,6 +57,27 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
+
+// 4x4 transpose of words across the four 16-lane rows of a wave: word a of
+// row b becomes word b of row a.
+__device__ __forceinline__ void xpose4(uint32_t* w) {
+  const auto r = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  const auto q = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  const auto u = __builtin_amdgcn_permlane16_swap(r[0], q[0], false, false);
+  const auto v = __builtin_amdgcn_permlane16_swap(r[1], q[1], false, false);
+  w[0] = u[0];
+  w[1] = u[1];
+  w[2] = v[0];
+  w[3] = v[1];
+}
+
+// Raw buffer descriptor over `bytes` bytes (gfx9-family raw format word):
+// loads at offsets >= bytes return zeros without a memory access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_buf(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+// OR-ed into an offset it puts it past every tensor (all are < 2 GiB).
+constexpr uint32_t kOob = 0xFFFFF000u;
 
 // Up to kSkMaxParts weight sets on one x per launch (q/k/v): workgroup b
 // takes tile b - tile0 of the part whose range holds b. In paired mode (the
@@ -66,27 +97,30 @@ struct SkParts {
   int n, act;
 };
 
+// One piece's operands in registers: the lane's 32 codes per tile and x for
+// the four MFMA steps per m-tile.
 template <int BITS, int NTW, int MT>
 struct Piece {
-  u32x4 q[NTW][BITS / 4];  // the lane's 32 codes per tile
-  u32x4 x[MT][4];          // x[m, run .. run+31] per 16-row m-tile
+  u32x4 q[NTW][BITS / 4];
+  u32x4 x[MT][4];
 };
 
-template <int BITS, bool XBF16, bool SBF16, int GS, int NTW, int MT>
+template <int BITS, bool XBF16, bool SBF16, int GS, int NTW, int MT, int D>
 __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
     const uint16_t* __restrict__ x, SkParts parts, int M, int K, int ppw) {
-  constexpr int GP = kPiece / GS;               // groups per piece
+  using P_t = Piece<BITS, NTW, MT>;
+  constexpr int GP = kPiece / GS;  // groups per piece
   constexpr bool SPLIT = XBF16 && BITS == 8;    // 8-bit codes as two nibble operands
   constexpr uint32_t MAG = XBF16 ? 0x43004300u : 0x64006400u;   // OFF in both halves
   constexpr uint32_t ONE = XBF16 ? 0x3F803F80u : 0x3C003C00u;   // 1.0 in both halves
   constexpr float OFF = SPLIT ? 17.f * 128.f : (XBF16 ? 128.f : 1024.f);
-  using P_t = Piece<BITS, NTW, MT>;
-  constexpr int ROWS = 16 * NTW;
 
   // LDS: the scales and biases of the workgroup's rows for all of K
-  // ([2][ROWS][G] 16-bit values, loaded once), then the partial tiles of the
-  // cross-wave sum ([W][MT][NTW][4][64] floats).
+  // ([2][ROWS][G] 16-bit values), then the partial tiles of the cross-wave
+  // sum ([W][MT][NTW][4][64] floats).
   extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int ROWS = 16 * NTW;
+  uint16_t* sbl = reinterpret_cast<uint16_t*>(smem);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
   const int col = lane & 15, kb = lane >> 4;
@@ -95,46 +129,58 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
   int pi = 0;                          // the part (independent mode)
   if (!paired)
     while (pi + 1 < parts.n && (int)blockIdx.x >= parts.part[pi + 1].tile0) ++pi;
-  const int n0 = paired ? (int)blockIdx.x * 16 * HALF : ((int)blockIdx.x - parts.part[pi].tile0) * ROWS;
+  const int n0 = paired ? (int)blockIdx.x * 16 * HALF : ((int)blockIdx.x - parts.part[pi].tile0) * 16 * NTW;
   const int G = K / GS;
-  const int wpr = K * BITS / 32;
-  const int gl = (kb * 32) / GS;  // group of this lane's run within a piece
+  const int rowb = K * BITS / 8;  // bytes per row of codes
 
   // slot t: its part and its first row (paired: slots 0..HALF-1 gate, the
   // rest up, over the same rows)
   auto slot_part = [&](int t) { return paired ? (t < HALF ? 0 : 1) : pi; };
   auto slot_row = [&](int t) { return n0 + (paired ? (t % HALF) : t) * 16; };
-  const uint32_t* wrow[NTW];
+  __amdgpu_buffer_rsrc_t wb[NTW];
+  uint32_t wro[NTW], rmask[NTW];  // byte offset of the lane's row; rows past N read zeros
 #pragma unroll
   for (int t = 0; t < NTW; ++t) {
     const SkPart& sp = parts.part[slot_part(t)];
-    wrow[t] = sp.w + (int64_t)min(slot_row(t) + col, sp.N - 1) * wpr;
+    wb[t] = sk_buf(sp.w, (uint32_t)((int64_t)sp.N * rowb));
+    const int r = slot_row(t) + col;
+    rmask[t] = r < sp.N ? 0u : kOob;
+    wro[t] = (uint32_t)min(r, sp.N - 1) * rowb;
   }
-  bool mval[MT];
-  const u32x4* xr[MT];
+  // x rows past M (padding of the m-tile) read zeros: the batch costs x
+  // bytes for its M rows only
+  uint32_t xro[MT], xmask[MT];
+  const __amdgpu_buffer_rsrc_t xb = sk_buf(x, (uint32_t)((int64_t)M * K * 2));
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    mval[mt] = mt * 16 + col < M;
-    xr[mt] = reinterpret_cast<const u32x4*>(x + (int64_t)min(mt * 16 + col, M - 1) * K);
+    const int m = mt * 16 + col;
+    xmask[mt] = m < M ? 0u : kOob;
+    xro[mt] = (uint32_t)min(m, M - 1) * K * 2;
   }
 
-  uint16_t* sbl = reinterpret_cast<uint16_t*>(smem);
-  float* red = reinterpret_cast<float*>(smem + (size_t)2 * ROWS * G * 2);
-
-  auto load = [&](P_t& P, int piece) {
-    const int run = piece * kPiece + kb * 32;  // first code of the lane's run
+  // The wave's i-th piece is piece wave + i*W of the row: a workgroup reads
+  // W consecutive pieces of each row at a time. Pieces i >= ppw read zeros
+  // (and add nothing). The offsets are selected without branches, so the
+  // compiler's waits for a piece leave the later pieces' loads in flight.
+  auto load = [&](P_t& P, int i) {
+    const uint32_t pmask = (uint32_t)((ppw - 1 - i) >> 31) & kOob;  // i >= ppw
+    const int piece = wave + i * W;
+    const uint32_t cofs = (uint32_t)piece * (kPiece * BITS / 8) + kb * (BITS * 4);
 #pragma unroll
     for (int t = 0; t < NTW; ++t) {
-      const u32x4* src = reinterpret_cast<const u32x4*>(wrow[t] + run * BITS / 32);
 #pragma unroll
-      for (int h = 0; h < BITS / 4; ++h) P.q[t][h] = __builtin_nontemporal_load(src + h);
+      for (int h = 0; h < BITS / 4; ++h)
+        P.q[t][h] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(wb[t], (wro[t] + cofs + 16 * h) | rmask[t] | pmask, 0, 2));
     }
-    // padding rows (m >= M) load nothing: their lanes read zeros, so the
-    // batch costs x bytes for its M rows only
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) P.x[mt][j] = mval[mt] ? xr[mt][(run >> 3) + j] : u32x4{0u, 0u, 0u, 0u};
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t xc = (uint32_t)(piece * kPiece + j * 32 + kb * 8) * 2;
+        P.x[mt][j] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(xb, (xro[mt] + xc) | xmask[mt] | pmask, 0, 0));
+      }
   };
 
   f32x4 acc[MT][NTW];
@@ -144,7 +190,27 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
     for (int t = 0; t < NTW; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const u32x4 ones = u32x4{ONE, ONE, ONE, ONE};
 
-  auto compute = [&](const P_t& P, int piece) {
+  // MFMA step j of a piece covers its codes j*32 .. j*32+31 (lane row kb:
+  // j*32 + kb*8 .. +7), inside one quantization group (group size >= 32).
+  auto compute = [&](P_t& P, int i) {
+    const int piece = min(wave + i * W, W * ppw - 1);  // pieces past the wave's read zeros
+    // lane row kb loaded codes kb*32 .. kb*32+31 (4 or 8 words); step j
+    // wants word kb of lane row j: a 4x4 transpose of words across rows
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) {
+      if constexpr (BITS == 4) {
+        uint32_t w[4] = {P.q[t][0][0], P.q[t][0][1], P.q[t][0][2], P.q[t][0][3]};
+        xpose4(w);
+        P.q[t][0] = u32x4{w[0], w[1], w[2], w[3]};
+      } else {
+        uint32_t e[4] = {P.q[t][0][0], P.q[t][0][2], P.q[t][1][0], P.q[t][1][2]};
+        uint32_t o[4] = {P.q[t][0][1], P.q[t][0][3], P.q[t][1][1], P.q[t][1][3]};
+        xpose4(e);
+        xpose4(o);
+        P.q[t][0] = u32x4{e[0], o[0], e[1], o[1]};
+        P.q[t][1] = u32x4{e[2], o[2], e[3], o[3]};
+      }
+    }
     f32x4 pa[MT][NTW][GP], pb[MT][NTW][GP], xs[MT][GP];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -156,6 +222,7 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
       }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const int g = (j * 32) / GS;
       // the code operands of step j, per tile
       u32x4 lo[NTW], hi[NTW];
 #pragma unroll
@@ -181,16 +248,12 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const u32x4 a = mval[mt] ? permute_x<BITS>(P.x[mt][j]) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 a = permute_x<BITS>(P.x[mt][j]);
+        xs[mt][g] = mfma16<XBF16>(a, ones, xs[mt][g]);
 #pragma unroll
-        for (int g = 0; g < GP; ++g) {
-          const u32x4 ag = (GP == 1 || gl == g) ? a : u32x4{0u, 0u, 0u, 0u};
-          xs[mt][g] = mfma16<XBF16>(ag, ones, xs[mt][g]);
-#pragma unroll
-          for (int t = 0; t < NTW; ++t) {
-            pa[mt][t][g] = mfma16<XBF16>(ag, lo[t], pa[mt][t][g]);
-            if constexpr (SPLIT) pb[mt][t][g] = mfma16<XBF16>(ag, hi[t], pb[mt][t][g]);
-          }
+        for (int t = 0; t < NTW; ++t) {
+          pa[mt][t][g] = mfma16<XBF16>(a, lo[t], pa[mt][t][g]);
+          if constexpr (SPLIT) pb[mt][t][g] = mfma16<XBF16>(a, hi[t], pb[mt][t][g]);
         }
       }
     }
@@ -213,44 +276,78 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
       }
   };
 
-  P_t A, B;
-  const int p0 = wave * ppw;
-  load(A, p0);
-  // the rows' scales and biases: one run of consecutive rows per part (two
-  // in paired mode, into LDS rows 0.. and 16*HALF..); rows past N are not
-  // loaded and their outputs are never stored
-  for (int r = 0; r < (paired ? 2 : 1); ++r) {
-    const SkPart& sp = parts.part[paired ? r : pi];
-    const int rows = paired ? 16 * HALF : ROWS, dst0 = paired ? r * 16 * HALF : 0;
-    const int nr = min(rows, sp.N - n0);
-    const int64_t cnt = (int64_t)nr * G;
-    const uint16_t* src[2] = {sp.scales + (int64_t)n0 * G, sp.biases + (int64_t)n0 * G};
-    uint16_t* dst[2] = {sbl + (int64_t)dst0 * G, sbl + ((int64_t)ROWS + dst0) * G};
-    if ((G & 7) == 0) {
-      for (int64_t i = threadIdx.x; i < 2 * cnt / 8; i += blockDim.x) {
-        const int a = i >= cnt / 8;
-        const int64_t j = i - a * (cnt / 8);
-        reinterpret_cast<u32x4*>(dst[a])[j] = reinterpret_cast<const u32x4*>(src[a])[j];
-      }
-    } else {
-      for (int64_t i = threadIdx.x; i < 2 * cnt; i += blockDim.x) {
-        const int a = i >= cnt;
-        const int64_t j = i - a * cnt;
-        dst[a][j] = src[a][j];
-      }
+  // Scales and biases of the workgroup's rows for all of K, staged in LDS
+  // ([2][ROWS][G] 16-bit values): one contiguous [rows][G] block per array
+  // and part, copied in 16-byte words (issued before the pieces' loads, so
+  // the wait for them leaves the pieces in flight).
+  constexpr int SREG = 2;  // staged words per thread held in registers
+  u32x4 sv[SREG];
+  const int srows = paired ? 16 * HALF : 16 * NTW;  // rows per part
+  const int scnt = (paired ? 4 : 2) * srows * G / 8;  // words over (part, array)
+  const bool svec = (G & 7) == 0;
+  if (svec) {
+#pragma unroll
+    for (int r = 0; r < SREG; ++r) {
+      const int i = min((int)threadIdx.x + r * (int)blockDim.x, scnt - 1);
+      const int per = srows * G / 8, blk = i / per, j = i - blk * per;  // blk = part * 2 + array
+      const SkPart& sp = parts.part[paired ? (blk >> 1) : pi];
+      const uint16_t* src = (blk & 1) ? sp.biases : sp.scales;
+      // rows past N repeat the last row's words (never used)
+      const int64_t e = min((int64_t)n0 * G + (int64_t)j * 8, (int64_t)sp.N * G - 8);
+      sv[r] = *reinterpret_cast<const u32x4*>(src + e);
     }
   }
-  __syncthreads();
-  for (int i = 0; i < ppw; i += 2) {
-    if (i + 1 < ppw) load(B, p0 + i + 1);
-    compute(A, p0 + i);
-    if (i + 1 >= ppw) break;
-    if (i + 2 < ppw) load(A, p0 + i + 2);
-    compute(B, p0 + i + 1);
+  P_t buf[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    load(buf[d], d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  {
+    const int per = srows * G / 8;
+    auto dst_of = [&](int i) {
+      const int blk = i / per, j = i - blk * per;
+      const int row0 = paired ? (blk >> 1) * 16 * HALF : 0;
+      return reinterpret_cast<u32x4*>(sbl + (int64_t)(blk & 1) * ROWS * G + (int64_t)row0 * G) + j;
+    };
+    if (svec) {
+#pragma unroll
+      for (int r = 0; r < SREG; ++r) {
+        const int i = (int)threadIdx.x + r * (int)blockDim.x;
+        if (i < scnt) *dst_of(i) = sv[r];
+      }
+      for (int i = (int)threadIdx.x + SREG * (int)blockDim.x; i < scnt; i += blockDim.x) {
+        const int blk = i / per, j = i - blk * per;
+        const SkPart& sp = parts.part[paired ? (blk >> 1) : pi];
+        const uint16_t* src = (blk & 1) ? sp.biases : sp.scales;
+        const int64_t e = min((int64_t)n0 * G + (int64_t)j * 8, (int64_t)sp.N * G - 8);
+        *dst_of(i) = *reinterpret_cast<const u32x4*>(src + e);
+      }
+    } else {
+      const int per16 = srows * G;
+      for (int i = threadIdx.x; i < scnt * 8; i += blockDim.x) {
+        const int blk = i / per16, j = i - blk * per16;
+        const SkPart& sp = parts.part[paired ? (blk >> 1) : pi];
+        const uint16_t* src = (blk & 1) ? sp.biases : sp.scales;
+        const int row0 = paired ? (blk >> 1) * 16 * HALF : 0;
+        sbl[(int64_t)(blk & 1) * ROWS * G + (int64_t)row0 * G + j] = src[min((int64_t)n0 * G + j, (int64_t)sp.N * G - 1)];
+      }
+    }
+    __syncthreads();
+  }
+  for (int i = 0; i < ppw; i += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      compute(buf[d], i + d);
+      // the refill goes out before the next piece's arithmetic
+      load(buf[d], i + d + D);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
   // Sum the W partial tiles in wave order. D lane l holds rows 4*(l/16)+e,
   // column l%16 of each 16x16 tile.
+  float* red = reinterpret_cast<float*>(smem + (size_t)2 * ROWS * G * 2);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -335,8 +432,12 @@ hipError_t launch_t(const QmvArgs* a, int n, int act, const SkinnyPlan& p) {
   }
   if (act >= 0) wgs = (a[0].N + 8 * NTW - 1) / (8 * NTW);
   const size_t lds = skinny_lds(p, a[0].K, GS);
-  hipLaunchKernelGGL((skinny_kernel<BITS, XBF16, SBF16, GS, NTW, MT>), dim3(wgs), dim3(64 * p.W), lds,
-                     a[0].stream, (const uint16_t*)a[0].x, parts, a[0].M, a[0].K, p.ppw);
+  if (p.ppw <= kSkDepth1Max)
+    hipLaunchKernelGGL((skinny_kernel<BITS, XBF16, SBF16, GS, NTW, MT, 1>), dim3(wgs), dim3(64 * p.W), lds,
+                       a[0].stream, (const uint16_t*)a[0].x, parts, a[0].M, a[0].K, p.ppw);
+  else
+    hipLaunchKernelGGL((skinny_kernel<BITS, XBF16, SBF16, GS, NTW, MT, 2>), dim3(wgs), dim3(64 * p.W), lds,
+                       a[0].stream, (const uint16_t*)a[0].x, parts, a[0].M, a[0].K, p.ppw);
   return hipGetLastError();
 }
 
@@ -389,20 +490,21 @@ bool skinny_supported(int64_t M, int64_t N, int64_t K, int bits, int gs) {
   // round of resident waves the GEMM is faster (measured), so M > 16 uses
   // this kernel only where ceil(N/16) * W waves fit (a rule on N and K only).
   if (M > 16 && (int64_t)((N + 15) / 16) * p.W > kSkMaxWavesMt2) return false;
-  // Each wave computes its pieces in sequence. Where that chain of MFMAs
-  // (per piece and 16-row tile: 4 steps x groups x m-tiles x (P + X, and
-  // the high nibbles of 8-bit codes)) is long, the launch is compute-bound
-  // with few waves in flight and the GEMM is faster: Qwen2.5-7B's down
-  // projection (8-bit gs32, K = 18944) at M = 17..32 took 84-94 us here
-  // against 45-47 on the GEMM. Bound: ~10 us of MFMA issue per wave.
-  const int64_t per_piece = 4 * (kPiece / gs) * p.mt * (bits == 8 ? 3 : 2);  // MFMAs per piece and tile
-  const int64_t chain = (int64_t)p.ppw * per_piece * p.ntw * 16;
+  // MFMAs per piece: 4 steps x m-tiles of P per tile (two with the nibble
+  // operands of 8-bit codes; bf16 x, the case the bounds are measured on),
+  // and the X sums shared by the wave's tiles.
+  const int64_t p_tile = 4 * p.mt * (bits == 8 ? 2 : 1), x_sums = 4 * p.mt;
+  // Each wave computes its pieces in sequence. Where that chain of MFMAs is
+  // long the launch is compute-bound with few waves in flight and the GEMM
+  // is faster: Qwen2.5-7B's down projection (8-bit gs32, K = 18944) at
+  // M = 17..32 took 84-94 us on a four-times longer chain than this kernel
+  // has now, against 45-47 on the GEMM. Bound: ~10 us of MFMA issue per wave.
+  const int64_t chain = (int64_t)p.ppw * (p_tile * p.ntw + x_sums) * 16;
   if (chain > kSkMaxChainCycles) return false;
-  // Over the launch the MFMA work per code byte is fixed by (bits, gs, m-tiles);
+  // Over the launch the MFMA work per code byte is fixed by (bits, m-tiles);
   // its lower fixed cost wins on small matrices, the GEMM's throughput on
-  // large ones: Qwen2.5-7B's gate (8-bit gs32, 68 MB) at M = 16 took 58 us
-  // here against ~44 on the GEMM, its q (13 MB) 16 against 28.
-  if ((N + 15) / 16 * (K / kPiece) * per_piece > kSkMaxMfma) return false;
+  // large ones (measured crossover).
+  if ((N + 15) / 16 * (K / kPiece) * (p_tile + x_sums) > kSkMaxMfma) return false;
   return skinny_lds(p, K, gs) <= kSkMaxLds;
 }
 
