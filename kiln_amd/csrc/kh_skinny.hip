@@ -387,24 +387,32 @@ struct SkinnyPlan {
   int W, ppw, ntw, mt;
 };
 
-// Most 16-row tiles per wave that fit the registers (from the compiler's
-// register counts: larger tilings spill).
+// Most 16-row tiles per wave that fit the registers with two pieces in
+// flight (from the compiler's register counts: larger tilings spill).
 constexpr int max_ntw(int bits, int gs, int mt) {
+  return mt == 1 ? (bits == 8 && gs == 32 ? 2 : 4) : (bits == 8 && gs == 32 ? 1 : 2);
+}
+// Widest tiling a single-part launch chooses (measured: wider tiles of one
+// matrix leave CUs without work before they save x loads).
+constexpr int pref_ntw(int bits, int gs, int mt) {
   return mt == 1 ? (bits == 4 ? (gs == 128 ? 4 : 2) : (gs == 32 ? 1 : 2))
                  : (bits == 4 && gs == 128 ? 2 : 1);
 }
 
 // W and the pieces per wave depend on K only, so a row's summation order
-// is the same for every M this kernel serves.
-SkinnyPlan plan_skinny(int M, int N, int K, int bits, int gs) {
+// is the same for every M this kernel serves. The tile width keeps at least
+// 2048 waves in a single-part launch; a multi-part launch (q|k|v) widens to
+// 1024 waves with the full register budget (measured: Llama-3-8B q|k|v at
+// M = 16..32 took 11-15 us against 14-22 us on one tile per wave).
+SkinnyPlan plan_skinny(int M, int N, int K, int bits, int gs, bool multi = false) {
   const int np = K / kPiece;
   int W = kSkMaxWaves;
   while (np % W) --W;
   SkinnyPlan p{W, np / W, 1, M > 16 ? 2 : 1};
-  // as many rows per workgroup as keeps the launch at >= 2048 waves
-  const int mx = max_ntw(bits, gs, p.mt);
-  if (mx >= 4 && (int64_t)((N + 63) / 64) * W >= 2048) p.ntw = 4;
-  else if (mx >= 2 && (int64_t)((N + 31) / 32) * W >= 2048) p.ntw = 2;
+  const int mx = multi ? max_ntw(bits, gs, p.mt) : pref_ntw(bits, gs, p.mt);
+  const int64_t thr = multi ? 1024 : 2048;
+  if (mx >= 4 && (int64_t)((N + 63) / 64) * W >= thr) p.ntw = 4;
+  else if (mx >= 2 && (int64_t)((N + 31) / 32) * W >= thr) p.ntw = 2;
   return p;
 }
 
@@ -523,7 +531,7 @@ hipError_t launch_skinny_multi(const QmvArgs* a, int n) {
   }
   // the tile width from the launch's total rows (the sums do not depend on
   // it), narrowed if its LDS would not fit
-  SkinnyPlan p = plan_skinny(a[0].M, (int)std::min<int64_t>(nsum, INT32_MAX), a[0].K, a[0].bits, a[0].gs);
+  SkinnyPlan p = plan_skinny(a[0].M, (int)std::min<int64_t>(nsum, INT32_MAX), a[0].K, a[0].bits, a[0].gs, n > 1);
   while (p.ntw > 1 && skinny_lds(p, a[0].K, a[0].gs) > kSkMaxLds) p.ntw /= 2;
   return a[0].bits == 4 ? launch_b<4>(a, n, -1, p) : launch_b<8>(a, n, -1, p);
 }
