@@ -518,6 +518,21 @@ __global__ void gemm_reduce(const float* __restrict__ part, void* __restrict__ o
   store_from_f32(out, odt, i, epi(s, i % N));
 }
 
+// The gated MLP after two split-K GEMMs (gate and up): each output sums its
+// slices in order as gemm_reduce does, takes its epilogue, and the pair goes
+// through the activation (act_mul rounds both to odt first, as the stored
+// intermediates of separate calls would be).
+__global__ void gemm_reduce_gate_up(const float* __restrict__ pg, int ng, const float* __restrict__ pu, int nu,
+                                    void* __restrict__ out, int odt, int64_t MN, int N, Epilogue eg,
+                                    Epilogue eu, int act) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= MN) return;
+  float g = pg[i], u = pu[i];
+  for (int k = 1; k < ng; ++k) g += pg[(int64_t)k * MN + i];
+  for (int k = 1; k < nu; ++k) u += pu[(int64_t)k * MN + i];
+  store_from_f32(out, odt, i, act_mul(eg(g, i % N), eu(u, i % N), odt, act));
+}
+
 }  // namespace
 
 GemmPlan plan_gemm(int M, int N, int K, int bits) {
@@ -609,7 +624,7 @@ static hipError_t launch_s(const QmvArgs& a, const GemmPlan& p, const u32x4* xh,
 
 // `xh`/`rsc` as written by launch_prep_x; `part` holds gemm_partial_bytes.
 hipError_t launch_gemm(const QmvArgs& a, const GemmPlan& p, const void* xh, const float* rsc,
-                       float* part) {
+                       float* part, bool reduce) {
   hipError_t e;
   const u32x4* x4 = static_cast<const u32x4*>(xh);
   const bool sf16 = a.sdt == DT_F16;
@@ -617,10 +632,18 @@ hipError_t launch_gemm(const QmvArgs& a, const GemmPlan& p, const void* xh, cons
     e = sf16 ? launch_s<4, true, false>(a, p, x4, rsc, part) : launch_s<4, false, false>(a, p, x4, rsc, part);
   else
     e = sf16 ? launch_s<8, true, false>(a, p, x4, rsc, part) : launch_s<8, false, false>(a, p, x4, rsc, part);
-  if (e != hipSuccess || p.nsplit == 1) return e;
+  if (e != hipSuccess || p.nsplit == 1 || !reduce) return e;
   const int64_t MN = (int64_t)a.M * a.N;
   hipLaunchKernelGGL(gemm_reduce, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, a.stream, part,
                      a.out, a.odt, MN, a.N, p.nsplit, a.epi());
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_reduce_gate_up(const QmvArgs& g, const GemmPlan& pg, const float* part_g,
+                                      const QmvArgs& u, const GemmPlan& pu, const float* part_u, int act) {
+  const int64_t MN = (int64_t)g.M * g.N;
+  hipLaunchKernelGGL(gemm_reduce_gate_up, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, g.stream, part_g,
+                     pg.nsplit, part_u, pu.nsplit, g.out, g.odt, MN, g.N, g.epi(), u.epi(), act);
   return hipGetLastError();
 }
 

@@ -156,8 +156,13 @@ GemmPlan plan_gemm(int M, int N, int K, int bits);
 bool gemm_supported(int K);
 size_t gemm_partial_bytes(const GemmPlan& p, int M, int N);
 // xh/rsc from launch_prep_x; part: gemm_partial_bytes(p) bytes (unused if 0).
+// reduce = false leaves a split-K launch's partial sums in part.
 hipError_t launch_gemm(const QmvArgs& a, const GemmPlan& p, const void* xh, const float* rsc,
-                       float* part);
+                       float* part, bool reduce = true);
+// act(gate) * up from the partial sums of two split-K launches (nsplit > 1
+// each) into g.out, bitwise as two reduced launches and launch_act_mul.
+hipError_t launch_gemm_reduce_gate_up(const QmvArgs& g, const GemmPlan& pg, const float* part_g,
+                                      const QmvArgs& u, const GemmPlan& pu, const float* part_u, int act);
 
 // Any dtype / alignment / transpose: one thread per output, fp32 fma chain.
 hipError_t launch_qmm_generic(const QmvArgs& a, bool transpose);

@@ -661,6 +661,30 @@ int gate_up(const char* op, kh_array* res, const kh_array* x, const kh_array* w_
     const hipError_t e = kh::launch_skinny_gate_up(g, u, activation);
     return e == hipSuccess ? KH_OK : hip_fail(op, e);
   }
+  // Two split-K GEMMs on one activation conversion, reduced together with
+  // the activation (the partials of both stay in the workspace).
+  if (gemm_path(g, true) && gemm_path(u, true) && g.sdt == u.sdt) {
+    const kh::GemmPlan pg = kh::plan_gemm((int)g.M, g.N, (int)g.K, g.bits);
+    const kh::GemmPlan pu = kh::plan_gemm((int)u.M, u.N, (int)u.K, u.bits);
+    if (pg.nsplit > 1 && pu.nsplit > 1) {
+      const int64_t M = g.M, K = g.K;
+      const size_t xb = (size_t)M * K * 2, rb = ((size_t)M * 4 + 255) / 256 * 256;
+      const size_t bg = (kh::gemm_partial_bytes(pg, (int)M, g.N) + 255) / 256 * 256;
+      const size_t bu = kh::gemm_partial_bytes(pu, (int)M, u.N);
+      Workspace ws;
+      if (!workspace(g.stream, (xb + rb + bg + bu + 3) / 4, &ws, &rc, op)) return rc;
+      char* base = reinterpret_cast<char*>(ws.data);
+      float* rsc = reinterpret_cast<float*>(base + xb);
+      float* part_g = reinterpret_cast<float*>(base + xb + rb);
+      float* part_u = reinterpret_cast<float*>(base + xb + rb + bg);
+      g.out = res->data;
+      hipError_t e = kh::launch_prep_x(g, base, rsc);
+      if (e == hipSuccess) e = kh::launch_gemm(g, pg, base, rsc, part_g, false);
+      if (e == hipSuccess) e = kh::launch_gemm(u, pu, base, rsc, part_u, false);
+      if (e == hipSuccess) e = kh::launch_gemm_reduce_gate_up(g, pg, part_g, u, pu, part_u, activation);
+      return e == hipSuccess ? KH_OK : hip_fail(op, e);
+    }
+  }
   // Composite: gate and up into intermediates of the result dtype (workspace
   // buffer 1; the matmuls use buffer 0), then the activation.
   const size_t esz = dtype_size(res->dtype), count = (size_t)g.M * g.N;

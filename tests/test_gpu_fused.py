@@ -101,16 +101,20 @@ def _gate_up_case(M, N, K, seed, bias):
 
 
 @pytest.mark.parametrize("act", [_lib.ACT_SILU, _lib.ACT_GELU_APPROX])
-@pytest.mark.parametrize("M", [1, 4, 12, 24])
+@pytest.mark.parametrize("M", [1, 4, 12, 24, 40, 300])
 def test_mlp_gate_up_fused_equals_composite(act, M):
     """On the fused launch (gate and up with the same scale dtype: the decode
     GEMV at M = 1, 4, the small-batch MFMA kernel in paired mode at M = 12,
-    24) and on the composite path (up's scales in the other 16-bit dtype,
+    24, two split-K GEMMs reduced together with the activation at M = 40,
+    300) and on the composite path (up's scales in the other 16-bit dtype,
     same values: two matmul launches, then the activation kernel) the result
     is bit-identical."""
     print(f"case mlp_gate_up act={act} M={M}", flush=True)
     N, K = 272, 2048
     xd, gate, up, up_bf, _ = _gate_up_case(M, N, K, 70 + M, False)
+    if M >= 40:
+        plan = ops.quantized_matmul_plan(M, N, K, 64, 4)
+        assert plan.startswith("gemm") and "nsplit=1 " not in plan, plan
     fused = ops.mlp_gate_up(xd, gate, up, act, 64, 4)
     comp = ops.mlp_gate_up(xd, gate, up_bf, act, 64, 4)
     assert fused.dtype == comp.dtype
