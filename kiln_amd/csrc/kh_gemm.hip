@@ -49,6 +49,7 @@ constexpr int kBN = kWaves * kNT * 16;  // 256
 constexpr int kXcds = 8;
 constexpr int kMaxMT = 8;     // largest m tile: 128 rows
 constexpr int kCUs = 256;     // MI355X compute units
+constexpr int kReduceParts = 4;
 
 __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
@@ -533,6 +534,28 @@ __global__ void gemm_reduce_gate_up(const float* __restrict__ pg, int ng, const 
   store_from_f32(out, odt, i, act_mul(eg(g, i % N), eu(u, i % N), odt, act));
 }
 
+// The split-K reductions of up to kReduceParts launches in one grid: thread
+// i serves the part whose element range holds i, exactly as gemm_reduce.
+struct ReduceParts {
+  const float* part[kReduceParts];
+  void* out[kReduceParts];
+  int odt[kReduceParts], N[kReduceParts], nsplit[kReduceParts];
+  int64_t MN[kReduceParts], start[kReduceParts + 1];
+  Epilogue epi[kReduceParts];
+  int n;
+};
+__global__ void gemm_reduce_multi(ReduceParts r) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= r.start[r.n]) return;
+  int p = 0;
+  while (p + 1 < r.n && g >= r.start[p + 1]) ++p;
+  const int64_t i = g - r.start[p], MN = r.MN[p];
+  const float* part = r.part[p];
+  float s = part[i];
+  for (int k = 1; k < r.nsplit[p]; ++k) s += part[(int64_t)k * MN + i];
+  store_from_f32(r.out[p], r.odt[p], i, r.epi[p](s, i % r.N[p]));
+}
+
 }  // namespace
 
 GemmPlan plan_gemm(int M, int N, int K, int bits) {
@@ -644,6 +667,25 @@ hipError_t launch_gemm_reduce_gate_up(const QmvArgs& g, const GemmPlan& pg, cons
   const int64_t MN = (int64_t)g.M * g.N;
   hipLaunchKernelGGL(gemm_reduce_gate_up, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, g.stream, part_g,
                      pg.nsplit, part_u, pu.nsplit, g.out, g.odt, MN, g.N, g.epi(), u.epi(), act);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_reduce_multi(const QmvArgs* a, const GemmPlan* p, float* const* part, int n) {
+  if (n < 1 || n > kReduceParts) return hipErrorInvalidValue;
+  ReduceParts r{};
+  r.n = n;
+  r.start[0] = 0;
+  for (int i = 0; i < n; ++i) {
+    r.part[i] = part[i];
+    r.out[i] = a[i].out;
+    r.odt[i] = a[i].odt;
+    r.N[i] = a[i].N;
+    r.nsplit[i] = p[i].nsplit;
+    r.MN[i] = (int64_t)a[i].M * a[i].N;
+    r.epi[i] = a[i].epi();
+    r.start[i + 1] = r.start[i] + r.MN[i];
+  }
+  hipLaunchKernelGGL(gemm_reduce_multi, dim3((unsigned)((r.start[n] + 255) / 256)), dim3(256), 0, a[0].stream, r);
   return hipGetLastError();
 }
 

@@ -161,6 +161,9 @@ hipError_t launch_gemm(const QmvArgs& a, const GemmPlan& p, const void* xh, cons
                        float* part, bool reduce = true);
 // act(gate) * up from the partial sums of two split-K launches (nsplit > 1
 // each) into g.out, bitwise as two reduced launches and launch_act_mul.
+// The reductions of n <= 4 split-K launches (nsplit > 1 each, partial sums
+// in part[i]) in one launch, each output as launch_gemm's own reduction.
+hipError_t launch_gemm_reduce_multi(const QmvArgs* a, const GemmPlan* p, float* const* part, int n);
 hipError_t launch_gemm_reduce_gate_up(const QmvArgs& g, const GemmPlan& pg, const float* part_g,
                                       const QmvArgs& u, const GemmPlan& pu, const float* part_u, int act);
 

@@ -373,22 +373,43 @@ bool gemm_path(const kh::QmvArgs& a, bool transpose) {
 int run_gemm_parts(const char* op, const kh::QmvArgs* a, int n) {
   int rc;
   const int64_t M = a[0].M, K = a[0].K;
-  size_t part = 0;
+  std::vector<kh::GemmPlan> plan(n);
+  int nsplit_parts = 0;
+  size_t part = 0, part_sum = 0;
   for (int i = 0; i < n; ++i) {
-    const kh::GemmPlan p = kh::plan_gemm((int)M, a[i].N, (int)K, a[i].bits);
-    part = std::max(part, kh::gemm_partial_bytes(p, (int)M, a[i].N));
+    plan[i] = kh::plan_gemm((int)M, a[i].N, (int)K, a[i].bits);
+    const size_t b = kh::gemm_partial_bytes(plan[i], (int)M, a[i].N);
+    part = std::max(part, b);
+    part_sum += (b + 255) / 256 * 256;
+    nsplit_parts += plan[i].nsplit > 1;
   }
+  // Two or more split-K parts keep their partial sums side by side and are
+  // reduced by one launch; otherwise each launch reduces its own.
+  const bool joint = nsplit_parts >= 2 && n <= 4;
   // workspace: float16 activations | per-row scales | split-K partials
   const size_t xb = (size_t)M * K * 2, rb = ((size_t)M * 4 + 255) / 256 * 256;
   Workspace ws;
-  if (!workspace(a[0].stream, (xb + rb + part + 3) / 4, &ws, &rc, op)) return rc;
+  if (!workspace(a[0].stream, (xb + rb + (joint ? part_sum : part) + 3) / 4, &ws, &rc, op)) return rc;
   char* base = reinterpret_cast<char*>(ws.data);
   float* rsc = reinterpret_cast<float*>(base + xb);
   hipError_t e = kh::launch_prep_x(a[0], base, rsc);
+  kh::QmvArgs ra[4];
+  kh::GemmPlan rp[4];
+  float* rpart[4];
+  int nr = 0;
+  size_t off = xb + rb;
   for (int i = 0; i < n && e == hipSuccess; ++i) {
-    const kh::GemmPlan p = kh::plan_gemm((int)M, a[i].N, (int)K, a[i].bits);
-    e = kh::launch_gemm(a[i], p, base, rsc, reinterpret_cast<float*>(base + xb + rb));
+    float* pbuf = reinterpret_cast<float*>(base + (joint ? off : xb + rb));
+    const bool defer = joint && plan[i].nsplit > 1;
+    e = kh::launch_gemm(a[i], plan[i], base, rsc, pbuf, !defer);
+    if (defer) {
+      ra[nr] = a[i];
+      rp[nr] = plan[i];
+      rpart[nr++] = pbuf;
+      off += (kh::gemm_partial_bytes(plan[i], (int)M, a[i].N) + 255) / 256 * 256;
+    }
   }
+  if (e == hipSuccess && nr > 0) e = kh::launch_gemm_reduce_multi(ra, rp, rpart, nr);
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
 }
 
