@@ -101,17 +101,33 @@ struct ScaleChunk {
   static_assert(OPS * 64 * KW == 2 * BN * PIECES, "every wave issues the same loads");
 };
 
+// One weight matrix of a launch: its work items are start .. start +
+// cnt * (256 / BN) * nsplit - 1 of the launch (several parts sharing x, M, K
+// and the kernel class run as one launch; each part's results are those of
+// its own launch).
+struct GemmPart {
+  const uint32_t* w;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  float* part;
+  void* out;
+  int odt, N, kslice, tiles_n, tile0, cnt, nsplit, start;
+  Epilogue epi;
+};
+constexpr int kGemmParts = 4;
+struct GemmParts {
+  GemmPart p[kGemmParts];
+  int n, total;
+};
+
 // GR (grouped, gather_qmm): x holds the rows of every expert group, each
 // group padded to whole m-tiles; gtab[0] is the number of m-tiles in use and
 // gtab[1 + tm] the expert of m-tile tm (w, scales and biases are [E, N, ..]
 // stacks); rowmap[m] is the output row of padded row m, or -1 for padding.
 template <int BITS, bool SF16, int MT, int GS, int NT, bool GR>
 __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
-    const u32x4* __restrict__ xh, const float* __restrict__ rscale,
-    const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
-    const uint16_t* __restrict__ biases, float* __restrict__ part, void* __restrict__ out,
-    int odt, int M, int N, int K, int kslice, int tiles_n, int tile0, int cnt, int nsplit,
-    const int* __restrict__ gtab, const int* __restrict__ rowmap, Epilogue epi) {
+    const u32x4* __restrict__ xh, const float* __restrict__ rscale, GemmParts gp, int M, int K,
+    const int* __restrict__ gtab, const int* __restrict__ rowmap) {
   // NT 16-column MFMA tiles per wave: 4 (a 256-column tile) or 2 (half of
   // one, for the last partial round of a launch)
   constexpr int KW = kWaves;               // waves per workgroup
@@ -140,11 +156,23 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   // Grouped: only the m-tiles in use (a device-side count) are dealt out, so
   // they spread over all XCDs; the grid was sized for the most there can be.
   const int tiles_m = GR ? gtab[0] : (M + BM - 1) / BM;
-  const int total = GR ? tiles_m * tiles_n * SUB : cnt * SUB * nsplit;
+  const int total = GR ? tiles_m * gp.p[0].tiles_n * SUB : gp.total;
   const int per = (total + kXcds - 1) / kXcds;
   if (GR && (int)blockIdx.x / kXcds >= per) return;
-  const int t = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  int t = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
   if (t >= total) return;
+  // the part holding work item t (uniform)
+  int pi = 0;
+  while (pi + 1 < gp.n && t >= gp.p[pi + 1].start) ++pi;
+  t -= gp.p[pi].start;
+  const uint32_t* __restrict__ w = gp.p[pi].w;
+  const uint16_t* __restrict__ scales = gp.p[pi].scales;
+  const uint16_t* __restrict__ biases = gp.p[pi].biases;
+  float* __restrict__ part = gp.p[pi].part;
+  void* __restrict__ out = gp.p[pi].out;
+  const int odt = gp.p[pi].odt, N = gp.p[pi].N, kslice = gp.p[pi].kslice, tiles_n = gp.p[pi].tiles_n;
+  const int tile0 = gp.p[pi].tile0, cnt = gp.p[pi].cnt, nsplit = gp.p[pi].nsplit;
+  const Epilogue epi = gp.p[pi].epi;
   const int u0 = t % (cnt * SUB);
   const int sp = t / (cnt * SUB);
   const int tile = tile0 + u0 / SUB;
@@ -593,17 +621,31 @@ size_t gemm_partial_bytes(const GemmPlan& p, int M, int N) {
 
 bool gemm_supported(int K) { return K % kStage == 0; }
 
+GemmPart part_of(const QmvArgs& a, const GemmPlan& p, float* part, int tile0, int cnt, int nsplit, int start,
+                 bool gr) {
+  return GemmPart{(const uint32_t*)a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, part, a.out,
+                  a.odt, a.N, p.kslice, p.tiles_n, tile0, cnt, nsplit, start,
+                  gr ? Epilogue{nullptr, 0, 0} : a.epi()};
+}
+
+template <int BITS, bool SF16, int MT, int GS, int NT, bool GR>
+static hipError_t launch_parts(const GemmParts& gp, const QmvArgs& a, const u32x4* xh, const float* rsc,
+                               const int* gtab, const int* rowmap) {
+  const int grid = ((gp.total + kXcds - 1) / kXcds) * kXcds;
+  hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS, NT, GR>), dim3(grid), dim3(64 * kWaves), 0, a.stream, xh,
+                     rsc, gp, a.M, a.K, gtab, rowmap);
+  return hipGetLastError();
+}
+
 template <int BITS, bool SF16, int MT, int GS, int NT, bool GR>
 static hipError_t launch_range(const QmvArgs& a, const GemmPlan& p, const u32x4* xh,
                                const float* rsc, float* part, int tile0, int cnt, int nsplit,
                                const int* gtab, const int* rowmap) {
-  const int total = cnt * (kNT / NT) * nsplit;
-  const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
-  hipLaunchKernelGGL((gemm_kernel<BITS, SF16, MT, GS, NT, GR>), dim3(grid), dim3(64 * kWaves), 0,
-                     a.stream, xh, rsc, (const uint32_t*)a.w, (const uint16_t*)a.scales,
-                     (const uint16_t*)a.biases, part, a.out, a.odt, a.M, a.N, a.K, p.kslice,
-                     p.tiles_n, tile0, cnt, nsplit, gtab, rowmap, GR ? Epilogue{nullptr, 0, 0} : a.epi());
-  return hipGetLastError();
+  GemmParts gp{};
+  gp.n = 1;
+  gp.total = cnt * (kNT / NT) * nsplit;
+  gp.p[0] = part_of(a, p, part, tile0, cnt, nsplit, 0, GR);
+  return launch_parts<BITS, SF16, MT, GS, NT, GR>(gp, a, xh, rsc, gtab, rowmap);
 }
 
 template <int BITS, bool SF16, int MT, int GS, bool GR>
@@ -643,6 +685,52 @@ static hipError_t launch_s(const QmvArgs& a, const GemmPlan& p, const u32x4* xh,
     case 64: return launch_g<BITS, SF16, 64, GR>(a, p, xh, rsc, part, gtab, rowmap);
     default: return launch_g<BITS, SF16, 128, GR>(a, p, xh, rsc, part, gtab, rowmap);
   }
+}
+
+template <int BITS, bool SF16, int GS>
+static hipError_t multi_mt(const GemmParts& gp, const QmvArgs& a, int mt, const u32x4* xh, const float* rsc) {
+  switch (mt) {
+    case 1: return launch_parts<BITS, SF16, 1, GS, kNT, false>(gp, a, xh, rsc, nullptr, nullptr);
+    case 2: return launch_parts<BITS, SF16, 2, GS, kNT, false>(gp, a, xh, rsc, nullptr, nullptr);
+    case 4: return launch_parts<BITS, SF16, 4, GS, kNT, false>(gp, a, xh, rsc, nullptr, nullptr);
+    default: return launch_parts<BITS, SF16, 8, GS, kNT, false>(gp, a, xh, rsc, nullptr, nullptr);
+  }
+}
+template <int BITS, bool SF16>
+static hipError_t multi_gs(const GemmParts& gp, const QmvArgs& a, int mt, const u32x4* xh, const float* rsc) {
+  switch (a.gs) {
+    case 32: return multi_mt<BITS, SF16, 32>(gp, a, mt, xh, rsc);
+    case 64: return multi_mt<BITS, SF16, 64>(gp, a, mt, xh, rsc);
+    default: return multi_mt<BITS, SF16, 128>(gp, a, mt, xh, rsc);
+  }
+}
+
+bool gemm_multi_compatible(const QmvArgs* a, const GemmPlan* p, int n) {
+  if (n < 1 || n > kGemmParts) return false;
+  for (int i = 0; i < n; ++i)
+    if (a[i].bits != a[0].bits || a[i].gs != a[0].gs || a[i].sdt != a[0].sdt || p[i].mt != p[0].mt ||
+        p[i].tail != 0)
+      return false;
+  return true;
+}
+
+hipError_t launch_gemm_multi(const QmvArgs* a, const GemmPlan* p, const void* xh, const float* rsc,
+                             float* const* part, int n) {
+  if (!gemm_multi_compatible(a, p, n)) return hipErrorInvalidValue;
+  GemmParts gp{};
+  gp.n = n;
+  int start = 0;
+  for (int i = 0; i < n; ++i) {
+    const int cnt = p[i].tiles_n * p[i].tiles_m;
+    gp.p[i] = part_of(a[i], p[i], part[i], 0, cnt, p[i].nsplit, start, false);
+    start += cnt * p[i].nsplit;
+  }
+  gp.total = start;
+  const u32x4* x4 = static_cast<const u32x4*>(xh);
+  const bool sf16 = a[0].sdt == DT_F16;
+  if (a[0].bits == 4)
+    return sf16 ? multi_gs<4, true>(gp, a[0], p[0].mt, x4, rsc) : multi_gs<4, false>(gp, a[0], p[0].mt, x4, rsc);
+  return sf16 ? multi_gs<8, true>(gp, a[0], p[0].mt, x4, rsc) : multi_gs<8, false>(gp, a[0], p[0].mt, x4, rsc);
 }
 
 // `xh`/`rsc` as written by launch_prep_x; `part` holds gemm_partial_bytes.

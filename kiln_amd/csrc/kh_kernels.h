@@ -161,6 +161,13 @@ hipError_t launch_gemm(const QmvArgs& a, const GemmPlan& p, const void* xh, cons
                        float* part, bool reduce = true);
 // act(gate) * up from the partial sums of two split-K launches (nsplit > 1
 // each) into g.out, bitwise as two reduced launches and launch_act_mul.
+// n <= 4 GEMMs on one converted x as one launch (same bits, group size,
+// scale dtype and m-tile, no tail launch: gemm_multi_compatible). Parts with
+// nsplit > 1 leave their partial sums in part[i] (launch_gemm_reduce_multi);
+// the others store their results.
+bool gemm_multi_compatible(const QmvArgs* a, const GemmPlan* p, int n);
+hipError_t launch_gemm_multi(const QmvArgs* a, const GemmPlan* p, const void* xh, const float* rsc,
+                             float* const* part, int n);
 // The reductions of n <= 4 split-K launches (nsplit > 1 each, partial sums
 // in part[i]) in one launch, each output as launch_gemm's own reduction.
 hipError_t launch_gemm_reduce_multi(const QmvArgs* a, const GemmPlan* p, float* const* part, int n);

@@ -383,9 +383,11 @@ int run_gemm_parts(const char* op, const kh::QmvArgs* a, int n) {
     part_sum += (b + 255) / 256 * 256;
     nsplit_parts += plan[i].nsplit > 1;
   }
-  // Two or more split-K parts keep their partial sums side by side and are
-  // reduced by one launch; otherwise each launch reduces its own.
-  const bool joint = nsplit_parts >= 2 && n <= 4;
+  // Compatible parts run as one GEMM launch; split-K parts then keep their
+  // partial sums side by side and one launch reduces them all (also for two
+  // or more split-K parts launched one by one).
+  const bool one_launch = n > 1 && kh::gemm_multi_compatible(a, plan.data(), n);
+  const bool joint = (one_launch && nsplit_parts >= 1) || (nsplit_parts >= 2 && n <= 4);
   // workspace: float16 activations | per-row scales | split-K partials
   const size_t xb = (size_t)M * K * 2, rb = ((size_t)M * 4 + 255) / 256 * 256;
   Workspace ws;
@@ -393,21 +395,26 @@ int run_gemm_parts(const char* op, const kh::QmvArgs* a, int n) {
   char* base = reinterpret_cast<char*>(ws.data);
   float* rsc = reinterpret_cast<float*>(base + xb);
   hipError_t e = kh::launch_prep_x(a[0], base, rsc);
+  std::vector<float*> pbuf(n);
   kh::QmvArgs ra[4];
   kh::GemmPlan rp[4];
   float* rpart[4];
   int nr = 0;
   size_t off = xb + rb;
-  for (int i = 0; i < n && e == hipSuccess; ++i) {
-    float* pbuf = reinterpret_cast<float*>(base + (joint ? off : xb + rb));
-    const bool defer = joint && plan[i].nsplit > 1;
-    e = kh::launch_gemm(a[i], plan[i], base, rsc, pbuf, !defer);
-    if (defer) {
+  for (int i = 0; i < n; ++i) {
+    pbuf[i] = reinterpret_cast<float*>(base + (joint ? off : xb + rb));
+    if (joint && plan[i].nsplit > 1) {
       ra[nr] = a[i];
       rp[nr] = plan[i];
-      rpart[nr++] = pbuf;
+      rpart[nr++] = pbuf[i];
       off += (kh::gemm_partial_bytes(plan[i], (int)M, a[i].N) + 255) / 256 * 256;
     }
+  }
+  if (one_launch) {
+    if (e == hipSuccess) e = kh::launch_gemm_multi(a, plan.data(), base, rsc, pbuf.data(), n);
+  } else {
+    for (int i = 0; i < n && e == hipSuccess; ++i)
+      e = kh::launch_gemm(a[i], plan[i], base, rsc, pbuf[i], !(joint && plan[i].nsplit > 1));
   }
   if (e == hipSuccess && nr > 0) e = kh::launch_gemm_reduce_multi(ra, rp, rpart, nr);
   return e == hipSuccess ? KH_OK : hip_fail(op, e);
@@ -700,8 +707,17 @@ int gate_up(const char* op, kh_array* res, const kh_array* x, const kh_array* w_
       float* part_u = reinterpret_cast<float*>(base + xb + rb + bg);
       g.out = res->data;
       hipError_t e = kh::launch_prep_x(g, base, rsc);
-      if (e == hipSuccess) e = kh::launch_gemm(g, pg, base, rsc, part_g, false);
-      if (e == hipSuccess) e = kh::launch_gemm(u, pu, base, rsc, part_u, false);
+      const kh::QmvArgs gu[2] = {g, u};
+      const kh::GemmPlan pgu[2] = {pg, pu};
+      float* const parts[2] = {part_g, part_u};
+      if (e == hipSuccess) {
+        if (kh::gemm_multi_compatible(gu, pgu, 2)) {
+          e = kh::launch_gemm_multi(gu, pgu, base, rsc, parts, 2);
+        } else {
+          e = kh::launch_gemm(g, pg, base, rsc, part_g, false);
+          if (e == hipSuccess) e = kh::launch_gemm(u, pu, base, rsc, part_u, false);
+        }
+      }
       if (e == hipSuccess) e = kh::launch_gemm_reduce_gate_up(g, pg, part_g, u, pu, part_u, activation);
       return e == hipSuccess ? KH_OK : hip_fail(op, e);
     }
