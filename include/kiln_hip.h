@@ -40,6 +40,16 @@
  *     boundary, as Kiln does at eval/async_eval (array.rs:460-475).
  *   - a stream is driven from one thread at a time; calls on different
  *     streams may run concurrently.
+ *   - device scratch: kernels that need scratch (the GEMM's float16
+ *     activations and split-K partials, the gate/up intermediates, the MoE
+ *     grouping plan) take it from a workspace kept per (device, stream). The
+ *     first call on a stream that needs more than the workspace holds calls
+ *     hipMalloc (under stream capture in relaxed capture mode); later calls
+ *     of the same or smaller size allocate nothing. A workspace that a graph
+ *     capture has used is never freed while the process runs: when it must
+ *     grow it is retired (kept allocated) so captured graphs stay valid, and
+ *     those buffers are released only at process exit. Callers that must
+ *     never allocate use kh_quantized_matmul_noalloc.
  *   - shapes follow MLX: x is [..., K] (leading dims flattened to M), w is
  *     [N, K*bits/32] uint32 with the lowest `bits` bits holding the lowest
  *     column, scales and biases are [N, K/group_size]. mode must be "affine"
