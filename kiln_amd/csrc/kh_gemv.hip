@@ -112,13 +112,39 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
   return SBF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
 }
 
-// Wave butterfly at lane offset O, then O/2, ..., 1. While more than one
-// partial remains (CNT > 1), a step halves the set each lane carries: the
-// lane with bit O clear keeps the lower half, its partner the upper half, and
-// each adds the partner's copy of the half it keeps; after log2(NV) steps
-// lane l carries partial l >> (6 - log2(NV)). Later steps sum that survivor.
-// Float addition is commutative, so both lanes of a pair form the same sum
-// and every output sees the same tree over the 64 lanes whatever NV is.
+// The partner of lane l in the butterfly step at offset O <= 8, fetched by
+// DPP within a row of 16 lanes: l ^ 1 and l ^ 2 (quad permutes), the mirror
+// of l within its 8 lanes (O = 4) and within its 16 lanes (O = 8). Each
+// pairs l with a lane whose bit O differs and whose bits above O agree, so
+// the four steps sum each group of 16 lanes exactly once.
+template <int O>
+__device__ __forceinline__ float dpp_partner(float v) {
+  constexpr int ctrl = O == 8 ? 0x140 : (O == 4 ? 0x141 : (O == 2 ? 0x4e : 0xb1));
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xf, 0xf, false));
+}
+
+// Lanes l and l + O (O = 32, 16) exchange a and b: after
+// v_permlane{32,16}_swap(a, b), lanes with bit O clear hold (own a, partner's
+// a) and lanes with bit O set hold (partner's b, own b), so the sum of the
+// pair is own + partner's copy of the half the lane keeps.
+template <int O>
+__device__ __forceinline__ float swap_sum(float a, float b) {
+  const unsigned ua = __builtin_bit_cast(unsigned, a), ub = __builtin_bit_cast(unsigned, b);
+  const auto r = O == 32 ? __builtin_amdgcn_permlane32_swap(ua, ub, false, false)
+                         : __builtin_amdgcn_permlane16_swap(ua, ub, false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+
+// Wave butterfly at lane offset O, then O/2, ..., 1, by cross-lane moves that
+// stay in the VALU (permlane swaps across 32 and 16 lanes, DPP below). While
+// more than one partial remains (CNT > 1), a step halves the set each lane
+// carries: the lane with bit O clear keeps the lower half, its partner the
+// upper half, and each adds the partner's copy of the half it keeps; after
+// log2(NV) steps lane l carries partial l >> (6 - log2(NV)). Later steps sum
+// that survivor. Float addition is commutative, so both lanes of a pair form
+// the same sum, and every output sees the same tree over the 64 lanes
+// whatever NV is.
 template <int CNT, int O>
 __device__ __forceinline__ void butterfly(float* acc, int lane) {
   if constexpr (O >= 1) {
@@ -127,13 +153,20 @@ __device__ __forceinline__ void butterfly(float* acc, int lane) {
       const bool up = (lane & O) != 0;
 #pragma unroll
       for (int j = 0; j < H; ++j) {
-        const float send = up ? acc[j] : acc[j + H];
-        const float keep = up ? acc[j + H] : acc[j];
-        acc[j] = keep + __shfl_xor(send, O);
+        if constexpr (O >= 16) {
+          acc[j] = swap_sum<O>(acc[j], acc[j + H]);
+        } else {
+          const float send = up ? acc[j] : acc[j + H];
+          const float keep = up ? acc[j + H] : acc[j];
+          acc[j] = keep + dpp_partner<O>(send);
+        }
       }
       butterfly<H, O / 2>(acc, lane);
     } else {
-      acc[0] += __shfl_xor(acc[0], O);
+      if constexpr (O >= 16)
+        acc[0] = swap_sum<O>(acc[0], acc[0]);
+      else
+        acc[0] += dpp_partner<O>(acc[0]);
       butterfly<1, O / 2>(acc, lane);
     }
   }
@@ -163,6 +196,7 @@ struct GemvParts {
 // (strides ew, es). An id outside [-E, E) (negative ids count from the end)
 // gives zero rows.
 constexpr int kGatherMaxDims = 8;
+constexpr int kModeOne = 0, kModeParts = 1, kModeGather = 2;
 struct GemvGather {
   const void* idx;
   int idx_signed, E, nrb, nd;
@@ -173,7 +207,9 @@ struct GemvGather {
 
 // RT rows per workgroup: R rows of one part, or (GU) R = RT/2 rows of the
 // gate and the same R rows of the up projection, stored as act(gate)*up.
-template <int BITS, bool XBF16, bool SBF16, int M, int RT, int I, bool GU>
+// MODE: kModeOne (one part), kModeParts (several parts on one x) or
+// kModeGather (gather mode: gth describes the pairs; otherwise it is unused).
+template <int BITS, bool XBF16, bool SBF16, int M, int RT, int I, bool GU, int MODE>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
     const uint16_t* __restrict__ x, const GemvParts parts, const GemvGather gth, int odt, int Mrows,
     int K, int cshift) {
@@ -194,18 +230,44 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
   const int wpr = nch * 4;           // words per row
   const int G = nch >> cshift;       // groups per row (cshift = log2(group_size / CPC))
   constexpr int RP = GU ? R / 2 : R;  // rows per part of this workgroup
-  int part = 0;                       // (GU: the gate's part; up is part 1)
-  if (!GU)
-    for (int i = 1; i < parts.nparts; ++i) part = (int)blockIdx.x >= parts.wg0[i] ? i : part;
-  const int N = parts.N[part];
-  int row0 = ((int)blockIdx.x - parts.wg0[part]) * RP;
+  // This workgroup's part (GU: the gate's part; up is part 1), chosen by
+  // selects over every slot of the table, so all kernel arguments are read
+  // in one batch of scalar loads with no load depending on another.
+  int part = 0;
+  if constexpr (!GU && MODE == kModeParts) {
+#pragma unroll
+    for (int i = 1; i < kGemvMaxParts; ++i)
+      part = (i < parts.nparts && (int)blockIdx.x >= parts.wg0[i]) ? i : part;
+  }
+  const uint32_t* wsel = parts.w[0];
+  const uint16_t* ssel = parts.scales[0];
+  const uint16_t* bsel = parts.biases[0];
+  void* osel = parts.out[0];
+  const void* bias_sel = parts.bias[0];
+  int bdt_sel = parts.bdt[0], N_sel = parts.N[0], wg0_sel = parts.wg0[0];
+  if constexpr (!GU && MODE == kModeParts) {
+#pragma unroll
+    for (int i = 1; i < kGemvMaxParts; ++i) {
+      const bool t = part == i;
+      wsel = t ? parts.w[i] : wsel;
+      ssel = t ? parts.scales[i] : ssel;
+      bsel = t ? parts.biases[i] : bsel;
+      osel = t ? parts.out[i] : osel;
+      bias_sel = t ? parts.bias[i] : bias_sel;
+      bdt_sel = t ? parts.bdt[i] : bdt_sel;
+      N_sel = t ? parts.N[i] : N_sel;
+      wg0_sel = t ? parts.wg0[i] : wg0_sel;
+    }
+  }
+  const int N = N_sel;
+  int row0 = ((int)blockIdx.x - wg0_sel) * RP;
   // operand pointers of this workgroup (h = 1: the up projection under GU)
   const uint16_t* xp = x;
-  const uint32_t* wp[2] = {parts.w[part], parts.w[GU ? 1 : part]};
-  const uint16_t* sp[2] = {parts.scales[part], parts.scales[GU ? 1 : part]};
-  const uint16_t* bp[2] = {parts.biases[part], parts.biases[GU ? 1 : part]};
-  void* outp = parts.out[part];
-  if (!GU && gth.idx != nullptr) {  // uniform
+  const uint32_t* wp[2] = {wsel, GU ? parts.w[1] : wsel};
+  const uint16_t* sp[2] = {ssel, GU ? parts.scales[1] : ssel};
+  const uint16_t* bp[2] = {bsel, GU ? parts.biases[1] : bsel};
+  void* outp = osel;
+  if constexpr (MODE == kModeGather) {
     const int pair = (int)blockIdx.x / gth.nrb;
     row0 = ((int)blockIdx.x % gth.nrb) * RP;
     int64_t xo = 0, io = 0;
@@ -350,7 +412,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_kernel(
     for (int v = 1; v < W; ++v) s += red[v][tid];
     const int r = tid / M, m = tid % M;
     const int n = row0 + r;
-    const Epilogue epi{parts.bias[part], parts.bdt[part], parts.ydt};
+    const Epilogue epi{bias_sel, bdt_sel, parts.ydt};
     if (n < N && m < Mrows) store_from_f32(outp, odt, (int64_t)m * N + n, epi(s, n));
   }
   if (GU && tid < NV / 2) {  // partial j = r*M + m: gate rows first, then up rows
@@ -401,15 +463,24 @@ hipError_t launch_one(const GemvLaunch& L, const GemvPlan& p) {
   const int cshift = __builtin_ctz(a.gs / CPC);
   if (L.gu) {
     if constexpr (2 * R * M <= 64)
-      hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, 2 * R, I, true>), dim3(L.total_wgs),
+      hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, 2 * R, I, true, kModeParts>), dim3(L.total_wgs),
                          dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, L.parts, L.gth, a.odt,
                          a.M, a.K, cshift);
     else
       return hipErrorInvalidValue;
   } else {
-    hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, R, I, false>), dim3(L.total_wgs),
-                       dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, L.parts, L.gth, a.odt, a.M,
-                       a.K, cshift);
+    if (L.gth.idx != nullptr)
+      hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, R, I, false, kModeGather>), dim3(L.total_wgs),
+                         dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, L.parts, L.gth, a.odt, a.M,
+                         a.K, cshift);
+    else if (L.parts.nparts > 1)
+      hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, R, I, false, kModeParts>), dim3(L.total_wgs),
+                         dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, L.parts, L.gth, a.odt, a.M,
+                         a.K, cshift);
+    else
+      hipLaunchKernelGGL((gemv_kernel<BITS, XBF16, SBF16, M, R, I, false, kModeOne>), dim3(L.total_wgs),
+                         dim3(64 * p.waves), 0, a.stream, (const uint16_t*)a.x, L.parts, L.gth, a.odt, a.M,
+                         a.K, cshift);
   }
   return hipGetLastError();
 }
