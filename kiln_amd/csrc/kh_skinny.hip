@@ -105,7 +105,9 @@ struct Piece {
   u32x4 x[MT][4];
 };
 
-template <int BITS, bool XBF16, bool SBF16, int GS, int NTW, int MT, int D>
+// SOLO: a launch of one part (no part table walk: every kernel argument is
+// read at a fixed offset, in one batch of scalar loads).
+template <int BITS, bool XBF16, bool SBF16, int GS, int NTW, int MT, int D, bool SOLO>
 __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
     const uint16_t* __restrict__ x, SkParts parts, int M, int K, int ppw) {
   using P_t = Piece<BITS, NTW, MT>;
@@ -124,11 +126,13 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void skinny_kernel(
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
   const int col = lane & 15, kb = lane >> 4;
-  const bool paired = parts.act >= 0;  // uniform
+  const bool paired = !SOLO && parts.act >= 0;  // uniform
   constexpr int HALF = NTW / 2 > 0 ? NTW / 2 : 1;  // tiles per part in paired mode (NTW even there)
   int pi = 0;                          // the part (independent mode)
-  if (!paired)
-    while (pi + 1 < parts.n && (int)blockIdx.x >= parts.part[pi + 1].tile0) ++pi;
+  if constexpr (!SOLO) {
+    if (!paired)
+      while (pi + 1 < parts.n && (int)blockIdx.x >= parts.part[pi + 1].tile0) ++pi;
+  }
   const int n0 = paired ? (int)blockIdx.x * 16 * HALF : ((int)blockIdx.x - parts.part[pi].tile0) * 16 * NTW;
   const int G = K / GS;
   const int rowb = K * BITS / 8;  // bytes per row of codes
@@ -440,12 +444,22 @@ hipError_t launch_t(const QmvArgs* a, int n, int act, const SkinnyPlan& p) {
   }
   if (act >= 0) wgs = (a[0].N + 8 * NTW - 1) / (8 * NTW);
   const size_t lds = skinny_lds(p, a[0].K, GS);
-  if (p.ppw <= kSkDepth1Max)
-    hipLaunchKernelGGL((skinny_kernel<BITS, XBF16, SBF16, GS, NTW, MT, 1>), dim3(wgs), dim3(64 * p.W), lds,
-                       a[0].stream, (const uint16_t*)a[0].x, parts, a[0].M, a[0].K, p.ppw);
-  else
-    hipLaunchKernelGGL((skinny_kernel<BITS, XBF16, SBF16, GS, NTW, MT, 2>), dim3(wgs), dim3(64 * p.W), lds,
-                       a[0].stream, (const uint16_t*)a[0].x, parts, a[0].M, a[0].K, p.ppw);
+  const bool one = n == 1 && act < 0;
+  if (p.ppw <= kSkDepth1Max) {
+    if (one)
+      hipLaunchKernelGGL((skinny_kernel<BITS, XBF16, SBF16, GS, NTW, MT, 1, true>), dim3(wgs), dim3(64 * p.W), lds,
+                         a[0].stream, (const uint16_t*)a[0].x, parts, a[0].M, a[0].K, p.ppw);
+    else
+      hipLaunchKernelGGL((skinny_kernel<BITS, XBF16, SBF16, GS, NTW, MT, 1, false>), dim3(wgs), dim3(64 * p.W), lds,
+                         a[0].stream, (const uint16_t*)a[0].x, parts, a[0].M, a[0].K, p.ppw);
+  } else {
+    if (one)
+      hipLaunchKernelGGL((skinny_kernel<BITS, XBF16, SBF16, GS, NTW, MT, 2, true>), dim3(wgs), dim3(64 * p.W), lds,
+                         a[0].stream, (const uint16_t*)a[0].x, parts, a[0].M, a[0].K, p.ppw);
+    else
+      hipLaunchKernelGGL((skinny_kernel<BITS, XBF16, SBF16, GS, NTW, MT, 2, false>), dim3(wgs), dim3(64 * p.W), lds,
+                         a[0].stream, (const uint16_t*)a[0].x, parts, a[0].M, a[0].K, p.ppw);
+  }
   return hipGetLastError();
 }
 
