@@ -427,6 +427,7 @@ size_t skinny_lds(const SkinnyPlan& p, int64_t K, int gs) {
 constexpr size_t kSkMaxLds = 96 * 1024;
 constexpr int64_t kSkMaxChainCycles = 20000;  // MFMA cycles per wave (measured bound, see skinny_supported)
 constexpr int64_t kSkMaxMfma = 1000000;        // MFMAs per launch (measured crossover, see skinny_supported)
+constexpr int64_t kSkMaxXBytes = (int64_t)150 << 20;  // x reads of a launch at M = 17..32 (measured, see skinny_supported)
 constexpr int64_t kSkMaxWavesMt2 = 3 * 4 * 256;  // three waves per SIMD on 256 CUs  // keeps at least one workgroup per CU with room to spare
 
 // One launch over n parts sharing x, M, K and the plan (act >= 0: paired
@@ -512,6 +513,11 @@ bool skinny_supported(int64_t M, int64_t N, int64_t K, int bits, int gs) {
   // round of resident waves the GEMM is faster (measured), so M > 16 uses
   // this kernel only where ceil(N/16) * W waves fit (a rule on N and K only).
   if (M > 16 && (int64_t)((N + 15) / 16) * p.W > kSkMaxWavesMt2) return false;
+  // Every 16-row tile reads all of x: at M = 17..32 a long-K matrix makes
+  // that stream several times the code bytes (Llama-3-8B down 4096x14336 at
+  // M = 32: 235 MB of x reads against 29 MB of codes, 31.7 us against 27.8
+  // on the GEMM; at M = 17, 125 MB, 22.9 us against 26.7).
+  if (M > 16 && (int64_t)((N + 15) / 16) * K * 2 * M > kSkMaxXBytes) return false;
   // MFMAs per piece: 4 steps x m-tiles of P per tile (two with the nibble
   // operands of 8-bit codes; bf16 x, the case the bounds are measured on),
   // and the X sums shared by the wave's tiles.
