@@ -285,7 +285,7 @@ def test_errors_raise_kiln_error():
 @pytest.mark.parametrize("M,N,K", [(1, 1024, 4096), (3, 272, 1024), (130, 200, 512), (24, 1024, 4096),
                                    (64, 8200, 2048)])
 def test_graph_capture_replays_match_eager(M, N, K):
-    """The library's launches (split-K counters, workspace) are capturable in a
+    """The library's launches (split-K partials, workspace) are capturable in a
     HIP graph; every replay, with eager work in between, equals the eager call."""
     print(f"case graph M={M} N={N} K={K}", flush=True)
     L, x = _case(M, N, K, 64, 4, seed=13)
