@@ -1,6 +1,8 @@
 // kh_common.h — shared device helpers for the gfx950 quantized-linear kernels.
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -52,6 +54,28 @@ __device__ __forceinline__ void store_from_f32(void* p, int dt, int64_t i, float
     uint32_t h = dt == DT_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
     static_cast<uint16_t*>(p)[i] = (uint16_t)h;
   }
+}
+
+// Maximum of v over the 64 lanes of a wave, in every lane, by cross-lane
+// moves that stay in the VALU: DPP within 16-lane rows (l ^ 1, l ^ 2, the
+// mirror within 8 and within 16 lanes), then v_permlane16_swap and
+// v_permlane32_swap across rows (a ds_bpermute per step would be a round
+// trip through the LDS crossbar). The maximum does not depend on the order.
+__device__ __forceinline__ float wave_max(float v) {
+  auto dpp = [](float a, auto ctrl) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0xb1>{}));
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x4e>{}));
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x141>{}));
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x140>{}));
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = fmaxf(__builtin_bit_cast(float, (unsigned)r16[0]), __builtin_bit_cast(float, (unsigned)r16[1]));
+  const unsigned w = __builtin_bit_cast(unsigned, v);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)r32[0]), __builtin_bit_cast(float, (unsigned)r32[1]));
 }
 
 // v rounded to dtype dt (round-to-nearest-even) and read back as float32.

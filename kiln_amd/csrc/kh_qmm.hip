@@ -144,8 +144,7 @@ __device__ __forceinline__ void prep_row_regs(const uint16_t* __restrict__ x, u3
       const float hi = XBF16 ? bf16_bits_to_f32(v[c][e] >> 16) : f16_bits_to_f32(v[c][e] >> 16);
       mx = fmaxf(mx, fmaxf(fabsf(lo), fabsf(hi)));
     }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  mx = wave_max(mx);
   if constexpr (WPR > 1) {
     if ((tr & 63) == 0) red[tr >> 6] = mx;
     __syncthreads();
