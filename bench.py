@@ -90,7 +90,9 @@ def main():
 
     def graph_us(fn, copies, reps):
         """Average µs of fn(c) over a graph holding fn(0..copies-1), replayed
-        `reps` times; HIP events on the capture/replay stream."""
+        `reps` times; HIP events on the capture/replay stream. Untimed
+        replays first (at least 5) bring the clocks back up after the host
+        work of the capture."""
         for c in range(copies):
             fn(c)
         torch.cuda.synchronize()
@@ -98,7 +100,8 @@ def main():
         with torch.cuda.graph(graph):
             for c in range(copies):
                 fn(c)
-        graph.replay()
+        for _ in range(max(5, reps // 4)):
+            graph.replay()
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
@@ -146,7 +149,7 @@ def main():
     nsteps = args.steps
     step_bytes = sum(call_bytes(N, K, 1, bits, gs) for _, N, K in shapes)
     value = step_bytes / (step_us * 1e-6) / 1e9
-    per_shape_us = {name: graph_us(per[name], copies, 20) for name, _, _ in shapes}
+    per_shape_us = {name: graph_us(per[name], copies, 50) for name, _, _ in shapes}
     dN, dK = next((N, K) for n, N, K in shapes if n == "gate")
     dom_us = per_shape_us["gate"]
     dom_bytes = call_bytes(dN, dK, 1, bits, gs)
