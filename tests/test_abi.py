@@ -336,3 +336,26 @@ def test_linear_multi_validation():
     assert "(31)" in _lib.last_error()
     assert call(res32, arr(None, A(_lib.FLOAT32, (32,)))) == 4
     assert call(res, None) == 4
+
+
+# Kernel choice for the benchmark's Llama-3-8B shapes (4-bit gs64, bf16 x,
+# f16 scales), read from the library's own plan (host logic, no GPU): the
+# decode GEMV at M = 1 and for the narrow k/v shape at M = 8, the small-batch
+# MFMA kernel at M = 8..32 unless its x reads would exceed 150 MiB (down at
+# M >= 22) or it would need more than three waves per SIMD (gate at M > 16),
+# the GEMM above (split-K at decode sizes, the half-width tail at M = 2048).
+@pytest.mark.parametrize("M,N,K,plan", [
+    (1, 14336, 4096, "gemv"),
+    (8, 1024, 4096, "gemv"),
+    (8, 4096, 4096, "skinny"),
+    (8, 14336, 4096, "skinny"),
+    (21, 4096, 14336, "skinny"),
+    (22, 4096, 14336, "gemm mt=2 nsplit=16 tail=0"),
+    (32, 4096, 4096, "skinny"),
+    (32, 14336, 4096, "gemm mt=2 nsplit=4 tail=0"),
+    (64, 14336, 4096, "gemm mt=4 nsplit=4 tail=0"),
+    (2048, 14336, 4096, "gemm mt=8 nsplit=1 tail=128"),
+])
+def test_kernel_choice_on_benchmark_shapes(M, N, K, plan):
+    from kiln_amd import ops
+    assert ops.quantized_matmul_plan(M, N, K, 64, 4) == plan
