@@ -754,3 +754,26 @@ def test_skinny_kernel_exact(oracle, bits, gs, xdt):
         L, x = _case(M, N, K, gs, bits, xdt=xdt, seed=M + N + K + bits)
         y = _run(L, x, gs, bits, xdt, "f16", "f32")
         _check_f32(oracle, L, x, gs, bits, xdt, "f16", y, rel=EXACT_REL)
+
+
+@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float32])
+def test_split_k_reduction_widths_agree(odt):
+    """The split-K reduction serves four outputs per thread where the output
+    is aligned for 4-element stores and the reduction is large (the
+    Llama-3-8B gate shape at M = 64), one otherwise: both sum every output's
+    slices in slice order, so an output buffer shifted by one element (one
+    output per thread) holds the same bits."""
+    from kiln_amd.workloads import make_linear_device
+    M, N, K, gs = 64, 14336, 4096, 64
+    plan = ops.quantized_matmul_plan(M, N, K, gs, 4)
+    assert plan.startswith("gemm") and "nsplit=1 " not in plan, plan
+    print(f"case split-K widths {plan} {odt}", flush=True)
+    L = make_linear_device(N, K, gs, "q4", seed=5, device=torch.device("cuda"))
+    x = torch.randn((M, K), generator=torch.Generator(device="cuda").manual_seed(6), device="cuda").bfloat16()
+    a = torch.empty((M, N), dtype=odt, device="cuda")
+    big = torch.empty(M * N + 1, dtype=odt, device="cuda")
+    b = big[1:].view(M, N)
+    ops.quantized_matmul(x, L["w"], L["scales"], L["biases"], True, gs, 4, out=a)
+    ops.quantized_matmul(x, L["w"], L["scales"], L["biases"], True, gs, 4, out=b)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
