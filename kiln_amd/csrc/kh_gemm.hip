@@ -50,6 +50,8 @@ constexpr int kXcds = 8;
 constexpr int kMaxMT = 8;     // largest m tile: 128 rows
 constexpr int kCUs = 256;     // MI355X compute units
 constexpr int kReduceParts = 4;
+// epilogue store kinds
+constexpr int kStPart = 0, kStBf16 = 1, kStF16 = 2, kStF32 = 3, kStAny = 4;
 
 __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
@@ -236,6 +238,19 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   for (int u = 0; u < NT; ++u) {
     const int n = n0 + wc * (NT * 16) + u * 16 + col;
     nrow[u] = n < N ? n : N - 1;
+  }
+  // The epilogue's per-row values (the activation row scale and, grouped,
+  // the output row), loaded now so that their latency hides behind the main
+  // loop rather than being paid at its end: lane l holds tile rows h*64+l.
+  constexpr int RR = (BM + 63) / 64;
+  float rsr[RR];
+  int rmr[RR];
+#pragma unroll
+  for (int h = 0; h < RR; ++h) {
+    const int m = m0 + h * 64 + lane;
+    const bool in = h * 64 + lane < BM && m < M;
+    rsr[h] = in ? rscale[m] : 0.f;
+    if constexpr (GR) rmr[h] = in ? rowmap[m] : -1;
   }
 
   // ---- loaders (all in bounds: indices past the slice or the matrix are
@@ -509,6 +524,20 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
   };
   // whole-block stores need 4 | N and 16-byte aligned base pointers
   const bool vec = (N & 3) == 0 && (((uintptr_t)out | (uintptr_t)part) & 15) == 0;
+  // Every global load the store loop needs is issued before it: vmcnt counts
+  // stores too, so a load between stores would wait for every store before
+  // it. A thread's four columns are the same in every round (64*KW blocks
+  // per round is a whole number of rows), so its bias values load once; the
+  // output rows of a pass load one per lane and travel by ds_bpermute.
+  constexpr int BQ = BN / 4;  // 16-byte blocks per row
+  static_assert((64 * KW) % BQ == 0, "fixed columns per thread");
+  const int cfix = (tid % BQ) * 4;
+  const bool add_bias = nsplit == 1 && epi.bias;  // uniform
+  float bv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (add_bias) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) bv[k] = load_as_f32(epi.bias, epi.bdt, min(n0 + cfix + k, N - 1));
+  }
 #pragma unroll
   for (int i0 = 0; i0 < MT; i0 += EP) {
     __syncthreads();
@@ -519,8 +548,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = (i - i0) * 16 + 4 * lg + e;
-        const int m = m0 + i * 16 + 4 * lg + e;
-        const float rs = m < M ? rscale[m] : 0.f;
+        const float rs = __shfl(rsr[i * 16 / 64], (i * 16 + 4 * lg + e) & 63);  // 0 past M
 #pragma unroll
         for (int u = 0; u < NT; ++u) T[tidx(r, wc * (NT * 16) + u * 16 + col)] = acc[il][u][e] * rs;
       }
@@ -528,39 +556,74 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_kernel(
     __syncthreads();
     constexpr int BLOCKS = EP * 16 * (BN / 4);  // 16-byte blocks of the pass
     static_assert(BLOCKS % (64 * KW) == 0, "whole rounds of blocks");
+    // One loop per kind of store, chosen once: the rounds are unrolled, and
+    // uniform tests inside them (split, alignment, dtype, bias) cost scalar
+    // branches and waits in every round.
+    auto store_rounds = [&](auto kind_c, auto bias_c) {
+      constexpr int KIND = decltype(kind_c)::value;
+      constexpr bool BIAS = decltype(bias_c)::value;
 #pragma unroll
-    for (int b0 = 0; b0 < BLOCKS; b0 += 64 * KW) {
-      const int b = b0 + tid, r = b / (BN / 4), c = (b % (BN / 4)) * 4;
-      int m = m0 + i0 * 16 + r;
-      const int n = n0 + c;
-      if (m >= M || n >= N) continue;
-      if constexpr (GR) {
-        m = rowmap[m];  // output row (split-K is never used here)
-        if (m < 0) continue;
-      }
-      f32x4 v = *reinterpret_cast<const f32x4*>(&T[tidx(r, c)]);
-      if (nsplit == 1 && epi.bias) {  // uniform
+      for (int b0 = 0; b0 < BLOCKS; b0 += 64 * KW) {
+        const int b = b0 + tid, r = b / BQ, c = cfix;
+        int m = m0 + i0 * 16 + r;
+        const int n = n0 + c;
+        if constexpr (GR) {
+          // output row (split-K is never used here); every lane takes part
+          const int rt = i0 * 16 + r;  // row in the tile
+          int g = __shfl(rmr[0], rt & 63);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) v[k] = epi(v[k], min(n + k, N - 1));
-      }
-      if (nsplit > 1) {
-        float* dst = part + ((int64_t)sp * M + m) * N + n;
-        if (vec) {
-          *reinterpret_cast<f32x4*>(dst) = v;
+          for (int h = 1; h < RR; ++h) {
+            const int gh = __shfl(rmr[h], rt & 63);
+            g = (rt >> 6) == h ? gh : g;
+          }
+          if (m >= M || n >= N || g < 0) continue;
+          m = g;
         } else {
-          for (int k = 0; k < 4 && n + k < N; ++k) dst[k] = v[k];
+          if (m >= M || n >= N) continue;
         }
-      } else if (vec && odt != DT_F32) {
-        const uint32_t lo = odt == DT_BF16 ? (f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16))
-                                           : (f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16));
-        const uint32_t hi = odt == DT_BF16 ? (f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16))
-                                           : (f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16));
-        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + (int64_t)m * N + n) = make_uint2(lo, hi);
-      } else if (vec) {
-        *reinterpret_cast<f32x4*>(static_cast<float*>(out) + (int64_t)m * N + n) = v;
-      } else {
-        for (int k = 0; k < 4 && n + k < N; ++k) store_from_f32(out, odt, (int64_t)m * N + n + k, v[k]);
+        f32x4 v = *reinterpret_cast<const f32x4*>(&T[tidx(r, c)]);
+        if constexpr (BIAS) {  // the same rounding as Epilogue
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[k] = round_to(v[k], epi.ydt) + bv[k];
+        }
+        if constexpr (KIND == kStPart) {
+          *reinterpret_cast<f32x4*>(part + ((int64_t)sp * M + m) * N + n) = v;
+        } else if constexpr (KIND == kStBf16 || KIND == kStF16) {
+          const int dt = KIND == kStBf16 ? DT_BF16 : DT_F16;
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + (int64_t)m * N + n) =
+              make_uint2(pack2(v[0], v[1], dt), pack2(v[2], v[3], dt));
+        } else if constexpr (KIND == kStF32) {
+          *reinterpret_cast<f32x4*>(static_cast<float*>(out) + (int64_t)m * N + n) = v;
+        } else {  // any layout, element by element
+          if (add_bias) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = round_to(v[k], epi.ydt) + bv[k];
+          }
+          for (int k = 0; k < 4 && n + k < N; ++k) {
+            if (nsplit > 1)
+              part[((int64_t)sp * M + m) * N + n + k] = v[k];
+            else
+              store_from_f32(out, odt, (int64_t)m * N + n + k, v[k]);
+          }
+        }
       }
+    };
+    using std::integral_constant;
+    using B0 = integral_constant<bool, false>;
+    using B1 = integral_constant<bool, true>;
+    if (!vec) {
+      store_rounds(integral_constant<int, kStAny>{}, B0{});
+    } else if (nsplit > 1) {  // no bias on partial sums
+      store_rounds(integral_constant<int, kStPart>{}, B0{});
+    } else if (odt == DT_BF16) {
+      if (add_bias) store_rounds(integral_constant<int, kStBf16>{}, B1{});
+      else store_rounds(integral_constant<int, kStBf16>{}, B0{});
+    } else if (odt == DT_F16) {
+      if (add_bias) store_rounds(integral_constant<int, kStF16>{}, B1{});
+      else store_rounds(integral_constant<int, kStF16>{}, B0{});
+    } else {
+      if (add_bias) store_rounds(integral_constant<int, kStF32>{}, B1{});
+      else store_rounds(integral_constant<int, kStF32>{}, B0{});
     }
   }
 }
