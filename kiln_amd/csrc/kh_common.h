@@ -25,9 +25,13 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
 
 // float -> bfloat16 bits, round-to-nearest-even; NaN stays a quiet NaN.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  // round to nearest even; NaN keeps its top bits with the quiet bit set.
+  // Both results are computed and one selected (an if compiles to an
+  // exec-mask branch per element).
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t qnan = (u >> 16) | 0x40u;
+  return (u & 0x7fffffffu) > 0x7f800000u ? qnan : rne;
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
