@@ -37,9 +37,10 @@ def _bias(N, dt, seed):
     return torch.from_numpy(b).to(dt).cuda()
 
 
-# (M, N, K, gs, bits): decode GEMV, skinny MFMA, GEMM split-K, GEMM, K % 128 != 0 (qmv / qmm)
+# (M, N, K, gs, bits): decode GEMV, skinny MFMA, GEMM split-K, GEMM, GEMM with N % 4 != 0 (the
+# element-by-element epilogue), K % 128 != 0 (qmv / qmm)
 PATHS = [(1, 272, 2048, 64, 4), (3, 96, 512, 32, 8), (12, 4096, 1024, 64, 4), (40, 300, 2048, 64, 4),
-         (200, 512, 512, 128, 4), (12, 96, 320, 64, 4), (40, 96, 320, 32, 8)]
+         (200, 512, 512, 128, 4), (256, 1022, 512, 64, 4), (12, 96, 320, 64, 4), (40, 96, 320, 32, 8)]
 
 
 @pytest.mark.parametrize("M,N,K,gs,bits", PATHS)
